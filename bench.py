@@ -1,0 +1,309 @@
+"""MoE-layer throughput on one MI355X, with the dominant kernel's roofline and a CPU baseline.
+
+A step is one pass of the routed MoE layer (router gemm -> topk_softmax -> moe_sort ->
+gather_gemm -> route_gemm -> moe_unpermute, through the library's C entries) over one batch of
+synthetic tokens already resident in HBM. The default workload is BASELINE.json configs[1]:
+Qwen3-30B-A3B-shaped layer, bf16, 64-token decode (H=2048, E=128, top-8, I=768), weights
+~N(0, 0.02) and activations ~N(0, 1) from a seed (near-uniform routing).
+
+Prints ONE JSON line. `value` is tokens/s of the whole layer; `roofline` is the dominant kernel's
+achieved algorithmic GB/s (decode) or TFLOP/s (prefill) from HIP events around its launches inside
+the timed region; `cpu_baseline` is the CPU oracle's restatement of the reference CPU formulas
+(`Fused::cpu`, crates/nn/src/functional/moe.rs) on the same inputs, timed on this host.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "uniserve-v1_amd"))
+
+METRIC = "MoE-layer tokens/s + % of HBM (decode) / MFMA (prefill) roofline, 1 GPU"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f8e4m3": 5000.0}  # dense
+
+CONFIGS = {
+    # name: tokens, hidden, experts, top, intermediate, weights, zipf routing
+    "30b-decode-bf16": (64, 2048, 128, 8, 768, "bf16", False),
+    "30b-prefill-bf16": (8192, 2048, 128, 8, 768, "bf16", True),
+    "30b-decode-fp8": (64, 2048, 128, 8, 768, "f8e4m3", False),
+    "30b-prefill-fp8": (8192, 2048, 128, 8, 768, "f8e4m3", True),
+    "235b-prefill-fp8": (4096, 4096, 128, 8, 1536, "f8e4m3", True),
+    "235b-decode-fp8": (1, 4096, 128, 8, 1536, "f8e4m3", False),
+}
+
+
+def parse():
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--config", default="30b-decode-bf16", choices=sorted(CONFIGS))
+    parser.add_argument("--extra", action="store_true", help="also measure every other BASELINE config")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    parser.add_argument("--cpu-runs", type=int, default=3)
+    return parser.parse_args()
+
+
+class Workload:
+    """Synthetic weights and tokens of one config, resident on the device."""
+
+    def __init__(self, name, seed=0):
+        import torch
+
+        from uniserve_moe import ops
+
+        self.name = name
+        (self.tokens, self.hidden, self.experts, self.top, self.intermediate, self.wdtype,
+         self.zipf) = CONFIGS[name]
+        device = torch.device("cuda:0")
+        g = torch.Generator(device=device).manual_seed(seed)
+
+        def normal(shape, std):
+            return (torch.randn(shape, generator=g, device=device) * std).to(torch.bfloat16)
+
+        T, H, E, I = self.tokens, self.hidden, self.experts, self.intermediate
+        self.x = normal((T, H), 1.0)
+        self.router = normal((E, H), 0.02)
+        self.up_gate_bf16 = normal((E, 2 * I, H), 0.02)
+        self.down_bf16 = normal((E, H, I), 0.02)
+        self.bias = None
+        if self.zipf:
+            self.bias = (-1.1 * torch.log(torch.arange(E, device=device, dtype=torch.float32) + 1.0)).contiguous()
+        self.scales = {}
+        if self.wdtype == "f8e4m3":
+            self.up_gate, s1 = quantize_blocks(self.up_gate_bf16)
+            self.down, s2 = quantize_blocks(self.down_bf16)
+            self.scales = dict(up_gate_scales=s1, down_scales=s2)
+        else:
+            self.up_gate, self.down = self.up_gate_bf16, self.down_bf16
+        self.layer = ops.MoeLayer(H, E, self.top, I, T, weight_dtype=self.wdtype)
+        self.out = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+
+    def step(self):
+        return self.layer(self.x, self.router, self.up_gate, self.down, out=self.out,
+                          router_bias=self.bias, **self.scales)
+
+
+def quantize_blocks(w):
+    """128 x 128 block-scaled e4m3 of a bf16 [E, N, K] stack on the device (setup, not timed):
+    scale = blockmax / 448, codes = e4m3fn(w / scale), torch's round-to-nearest-even cast."""
+    import torch
+
+    E, N, K = w.shape
+    blocks = w.float().reshape(E, N // 128, 128, K // 128, 128)
+    amax = blocks.abs().amax(dim=(2, 4), keepdim=True)
+    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    codes = (blocks / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return (codes.reshape(E, N, K).view(torch.uint8).contiguous(),
+            scale.reshape(E, N // 128, K // 128).contiguous())
+
+
+def measure(w, steps, warmup):
+    """Times `steps` layer calls (after `warmup`), and the FC1 / FC2 kernels inside them."""
+    import torch
+
+    from uniserve_moe import ops
+
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        w.step()
+    torch.cuda.synchronize()
+    # The whole layer: K back-to-back calls bracketed by synchronisations.
+    start = time.perf_counter()
+    for _ in range(steps):
+        w.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+
+    # The dominant kernels, launched as the layer launches them, timed with events on their stream.
+    maps_view = layer_maps(w)
+    rows = w.layer.views.permuted_rows
+    gated = w.layer.view("gated", torch.bfloat16, (rows, w.intermediate))
+    products = w.layer.view("products", torch.bfloat16, (rows, w.hidden))
+    fc = {"gather_gemm": [], "route_gemm": []}
+    if w.wdtype == "f8e4m3":
+        xq = w.layer.view("hidden_q", torch.uint8, (w.tokens, w.hidden))
+        xs = w.layer.view("hidden_s", torch.float32, (w.tokens, w.hidden // 128))
+        gq = w.layer.view("gated_q", torch.uint8, (rows, w.intermediate))
+        gs = w.layer.view("gated_s", torch.float32, (rows, w.intermediate // 128))
+        fc1 = lambda: ops.gather_gemm_fp8(xq, xs, w.up_gate, w.scales["up_gate_scales"], w.top, maps_view, rows, out=gated)  # noqa: E731
+        fc2 = lambda: ops.route_gemm_fp8(gq, gs, w.down, w.scales["down_scales"], maps_view, out=products)  # noqa: E731
+    else:
+        fc1 = lambda: ops.gather_gemm(w.x, w.up_gate, w.top, maps_view, rows, out=gated)  # noqa: E731
+        fc2 = lambda: ops.route_gemm(gated, w.down, maps_view, out=products)  # noqa: E731
+    for _ in range(max(3, warmup // 4)):
+        fc1()
+        fc2()
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        for name, fn in (("gather_gemm", fc1), ("route_gemm", fc2)):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            fc[name].append((a, b))
+    torch.cuda.synchronize()
+    kernel_ms = {name: sum(a.elapsed_time(b) for a, b in pairs) / len(pairs) for name, pairs in fc.items()}
+    return elapsed, kernel_ms
+
+
+def layer_maps(w):
+    """The layer workspace's sort maps as the [7, rows] view the entry wrappers take."""
+    import torch
+
+    from uniserve_moe import ops
+
+    v = w.layer.views
+    rows = v.permuted_rows
+
+    class Maps:
+        def __getitem__(self, index):
+            name = ["tile_to_expert", "tile_to_limit", "expanded_to_permuted", "permuted_to_expanded",
+                    "permuted_to_token", "total_padded_tokens", "num_non_exiting_tiles"][index]
+            length = {0: v.max_tiles, 1: v.max_tiles, 2: w.tokens * w.top, 3: rows, 4: rows, 5: 1, 6: 1}[index]
+            return w.layer.view(name, torch.int32, (length,))
+
+    del ops
+    return Maps()
+
+
+def algorithmic(w):
+    """Algorithmic bytes and flops of the layer and of FC1, from the run's own routing."""
+    import torch
+
+    ids = w.layer.view("ids", torch.int32, (w.tokens, w.top)).cpu()
+    touched = int(torch.unique(ids).numel())
+    routes = w.tokens * w.top
+    elem = 1 if w.wdtype == "f8e4m3" else 2
+    H, I, E, T = w.hidden, w.intermediate, w.experts, w.tokens
+    scale_bytes = 0
+    if w.wdtype == "f8e4m3":
+        scale_bytes = touched * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128)) * 4
+    layer_bytes = touched * 3 * H * I * elem + scale_bytes + T * H * 2 * 2 + H * E * 2
+    layer_flops = 2 * routes * 3 * H * I + 2 * T * H * E
+    act_elem = 1 if w.wdtype == "f8e4m3" else 2
+    fc1_bytes = touched * 2 * I * H * elem + T * H * act_elem + routes * I * 2
+    if w.wdtype == "f8e4m3":
+        fc1_bytes += touched * (2 * I // 128) * (H // 128) * 4 + T * (H // 128) * 4
+    fc1_flops = 2 * routes * 2 * I * H
+    return dict(touched=touched, layer_bytes=layer_bytes, layer_flops=layer_flops, fc1_bytes=fc1_bytes,
+                fc1_flops=fc1_flops)
+
+
+def cpu_baseline(w, runs):
+    """The CPU oracle (tests/oracle_lib.py over oracle/libmoe_oracle.so) on the same layer inputs."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    x, router = bits(w.x), bits(w.router)
+    if w.wdtype == "f8e4m3":
+        up_gate, down = w.up_gate.cpu().numpy(), w.down.cpu().numpy()
+        s1 = w.scales["up_gate_scales"].cpu().numpy()
+        s2 = w.scales["down_scales"].cpu().numpy()
+    else:
+        up_gate, down, s1, s2 = bits(w.up_gate), bits(w.down), None, None
+    oracle_lib.moe_layer(x[:1], router, up_gate, down, w.top, up_gate_scales=s1, down_scales=s2)  # warm
+    times = []
+    threads = 1
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        _, _, _, threads = oracle_lib.moe_layer(x, router, up_gate, down, w.top, up_gate_scales=s1, down_scales=s2)
+        times.append(time.perf_counter() - t0)
+    median = sorted(times)[len(times) // 2]
+    return {"value": round(w.tokens / median, 2), "unit": "tokens/s", "cores": int(threads), "kind": "port",
+            "sample": f"the whole {w.name} layer ({w.tokens} tokens), median of {runs} runs "
+                      f"({median * 1e3:.1f} ms each): C restatement of the reference's Fused::cpu formulas, "
+                      f"OpenMP over {threads} threads"}
+
+
+def run_config(name, steps, warmup, with_cpu, cpu_runs):
+    w = Workload(name)
+    elapsed, kernel_ms = measure(w, steps, warmup)
+    alg = algorithmic(w)
+    ms_per_step = elapsed / steps * 1e3
+    tokens_per_s = w.tokens * steps / elapsed
+    decode = not w.zipf and w.tokens <= 256
+    fc1_s = kernel_ms["gather_gemm"] * 1e-3
+    if decode:
+        achieved = alg["fc1_bytes"] / fc1_s / 1e9
+        roofline = {"kernel": "gather_gemm (FC1 + SiLU)", "bound": "hbm", "achieved": round(achieved, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "avg_launch_us": round(kernel_ms["gather_gemm"] * 1e3, 2)}
+    else:
+        achieved = alg["fc1_flops"] / fc1_s / 1e12
+        peak = MFMA_PEAK_TFLOPS[w.wdtype]
+        roofline = {"kernel": "gather_gemm (FC1 + SiLU)", "bound": "mfma", "achieved": round(achieved, 1),
+                    "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                    "avg_launch_us": round(kernel_ms["gather_gemm"] * 1e3, 2)}
+    layer = {
+        "ms_per_step": round(ms_per_step, 4),
+        "tokens_per_s": round(tokens_per_s, 1),
+        "layer_GBps": round(alg["layer_bytes"] / (ms_per_step * 1e-3) / 1e9, 1),
+        "layer_TFLOPs": round(alg["layer_flops"] / (ms_per_step * 1e-3) / 1e12, 2),
+        "layer_hbm_frac": round(alg["layer_bytes"] / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "layer_mfma_frac": round(alg["layer_flops"] / (ms_per_step * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS[w.wdtype], 4),
+        "touched_experts": alg["touched"],
+        "route_gemm_us": round(kernel_ms["route_gemm"] * 1e3, 2),
+        "gather_gemm_us": round(kernel_ms["gather_gemm"] * 1e3, 2),
+    }
+    cpu = cpu_baseline(w, cpu_runs) if with_cpu else None
+    return w, ms_per_step, tokens_per_s, roofline, layer, cpu
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: every box here has one MI355X and the layer "
+                          "holds all experts on it (expert-parallel sharding is a design note, not a path). "
+                          "Run with --gpus 1."}))
+        sys.exit(2)
+    import torch
+
+    w, ms_per_step, tokens_per_s, roofline, layer, cpu = run_config(
+        args.config, args.steps, args.warmup, not args.no_cpu, args.cpu_runs)
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.wdtype == "bf16" else "fp8-e4m3 (bf16 out)",
+        "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) weights)",
+        "config": {"workload": f"Qwen3-MoE layer {args.config}", "tokens": w.tokens, "hidden": w.hidden,
+                   "experts": w.experts, "top": w.top, "intermediate": w.intermediate,
+                   "routing": "zipf(1.1) bias" if w.zipf else "near-uniform", "parallelism": "single GPU, all experts resident"},
+        "roofline": roofline,
+        "layer": layer,
+        "cpu_baseline": cpu,
+        "device": torch.cuda.get_device_name(0),
+    }
+    if args.extra:
+        extra = {}
+        for name in CONFIGS:
+            if name == args.config:
+                continue
+            _, ms, tps, roof, lay, _ = run_config(name, max(10, args.steps // 10), max(3, args.warmup // 4), False, 0)
+            extra[name] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(tps, 1), "roofline": roof, "layer": lay}
+            torch.cuda.empty_cache()
+        line["extra"] = extra
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

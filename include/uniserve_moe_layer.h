@@ -1,0 +1,80 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The routed mixture-of-experts layer as one call: what `MoE::routed`
+// (crates/nn/src/modules/moe.rs:770-795) issues as six launches, in the same order and with the
+// same intermediate tensors - router gemm -> topk_softmax -> moe_sort -> gather_gemm ->
+// route_gemm -> moe_unpermute - on one stream, with every intermediate carved from one
+// caller-owned workspace so the call allocates nothing and can be captured into a graph.
+//
+// weight_dtype BF16: `up_gate` [E, 2I, H] (up rows then gate rows) and `down` [E, H, I] in bf16.
+// weight_dtype F8E4M3: both stacks e4m3 with FP32 128x128 block scales
+// (`up_gate_scales` [E, 2I/128, H/128], `down_scales` [E, H/128, I/128]); the activations are
+// quantised per row per 128 channels inside the call. The output is bf16 either way.
+
+#pragma once
+
+#include "uniserve_abi.h"
+
+struct uniserve_moe_layer_call {
+  const void *hidden;          ///< [tokens, hidden_size] bf16
+  const void *router;          ///< [experts, hidden_size] bf16
+  const void *up_gate;         ///< [experts, 2 * intermediate, hidden_size]
+  const void *down;            ///< [experts, hidden_size, intermediate]
+  const float *up_gate_scales; ///< fp8 only
+  const float *down_scales;    ///< fp8 only
+  const float *router_bias;    ///< [experts] added to the scores before rounding, or null
+  void *out;                   ///< [tokens, hidden_size] bf16
+  void *workspace;             ///< uniserve_moe_layer_workspace() bytes, 256-byte aligned
+  const int32_t *live_tokens;  ///< [1] live token rows, or null
+  int64_t workspace_bytes;
+  int64_t tokens;
+  int64_t hidden_size;
+  int64_t experts;
+  int64_t top;
+  int64_t intermediate;
+  int64_t renormalize;
+  int64_t weight_dtype;        ///< UNISERVE_DTYPE_BF16 or UNISERVE_DTYPE_F8E4M3
+  int64_t multiprocessors;
+  char error[512];
+};
+
+/// Workspace bytes the call needs for these extents, or -1 for extents it does not serve.
+UNISERVE_EXTERN_C int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_size,
+                                                       int64_t experts, int64_t top,
+                                                       int64_t intermediate, int64_t weight_dtype);
+
+/// Offsets (bytes from `workspace`) of the intermediate tensors, for callers that read them:
+/// scores, ids, weights, the seven sort maps, gated rows, products.
+struct uniserve_moe_layer_views {
+  int64_t scores;              ///< [tokens, experts] bf16
+  int64_t ids;                 ///< [tokens, top] i32
+  int64_t weights;             ///< [tokens, top] f32
+  int64_t tile_to_expert;      ///< [max_tiles] i32
+  int64_t tile_to_limit;       ///< [max_tiles] i32
+  int64_t expanded_to_permuted;///< [tokens, top] i32
+  int64_t permuted_to_expanded;///< [permuted_rows] i32
+  int64_t permuted_to_token;   ///< [permuted_rows] i32
+  int64_t total_padded_tokens; ///< [1] i32
+  int64_t num_non_exiting_tiles;///< [1] i32
+  int64_t gated;               ///< [permuted_rows, intermediate] bf16
+  int64_t products;            ///< [permuted_rows, hidden_size] bf16
+  int64_t hidden_q;            ///< fp8: [tokens, hidden_size] e4m3
+  int64_t hidden_s;            ///< fp8: [tokens, hidden_size / 128] f32
+  int64_t gated_q;             ///< fp8: [permuted_rows, intermediate] e4m3
+  int64_t gated_s;             ///< fp8: [permuted_rows, intermediate / 128] f32
+  int64_t max_tiles;
+  int64_t permuted_rows;
+  int64_t total;
+};
+
+UNISERVE_EXTERN_C int32_t uniserve_moe_layer_views_of(int64_t tokens, int64_t hidden_size,
+                                                      int64_t experts, int64_t top,
+                                                      int64_t intermediate, int64_t weight_dtype,
+                                                      struct uniserve_moe_layer_views *views);
+
+UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_call *call, void *stream);
+
+/// `ops::moe::max_tiles` (crates/ops/src/moe/mod.rs:63-70): the most tiles `tokens * top` routes
+/// over `local_experts` can fill at `tile` rows per tile.
+UNISERVE_EXTERN_C int64_t uniserve_moe_max_tiles(int64_t tokens, int64_t top, int64_t local_experts,
+                                                 int64_t tile);

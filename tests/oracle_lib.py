@@ -1,0 +1,251 @@
+"""numpy bindings of the CPU oracle (``oracle/libmoe_oracle.so``) - test infrastructure.
+
+Only the tests, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg load
+this module, and only as the checker.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+PATH = ROOT / "oracle" / "libmoe_oracle.so"
+if not PATH.exists():
+    raise RuntimeError(f"{PATH} is not built: run `make -C {PATH.parent}`")
+LIB = ctypes.CDLL(os.fspath(PATH))
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+
+
+def _sig(name, args, res=None):
+    fn = getattr(LIB, name)
+    fn.argtypes = args
+    fn.restype = res
+    return fn
+
+
+_sig("oracle_bf16_from_f32", [ctypes.c_float], ctypes.c_uint16)
+_sig("oracle_f32_from_bf16", [ctypes.c_uint16], ctypes.c_float)
+_sig("oracle_e4m3_from_f32", [ctypes.c_float], ctypes.c_uint8)
+_sig("oracle_f32_from_e4m3", [ctypes.c_uint8], ctypes.c_float)
+_sig("oracle_expf", [ctypes.c_float], ctypes.c_float)
+_sig("oracle_bf16_encode", [_P, _P, _I64])
+_sig("oracle_bf16_decode", [_P, _P, _I64])
+_sig("oracle_sequence", [_I64, ctypes.c_uint32, _P])
+_sig("oracle_normal", [_I64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, _P])
+_sig("oracle_normal_bf16", [_I64, ctypes.c_uint64, ctypes.c_float, _P])
+_sig("oracle_max_tiles", [_I64, _I64, _I64, _I64], _I64)
+_sig("oracle_topk_softmax", [_P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P])
+_sig("oracle_moe_sort", [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P])
+_sig("oracle_router_gemm", [_P, _P, _I64, _I64, _I64, _P])
+_sig("oracle_gather_gemm", [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P])
+_sig("oracle_route_gemm", [_P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
+_sig("oracle_moe_unpermute", [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P])
+_sig("oracle_quantize_rows_fp8", [_P, _I64, _I64, _I64, _P, _P])
+_sig("oracle_quantize_blocks_fp8", [_P, _I64, _I64, _I64, _I64, _P, _P])
+_sig("oracle_gather_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P])
+_sig("oracle_route_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
+_sig("oracle_moe_layer", [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P], _I32)
+_sig("oracle_threads", [], _I32)
+
+KINDS = {np.dtype(np.float32): 0, "bf16": 1, np.dtype(np.float16): 2}
+
+
+def _p(array):
+    return None if array is None else array.ctypes.data_as(_P)
+
+
+def _c(array, dtype):
+    return np.ascontiguousarray(array, dtype=dtype)
+
+
+def bf16_encode(values):
+    values = _c(values, np.float32)
+    out = np.empty(values.shape, dtype=np.uint16)
+    LIB.oracle_bf16_encode(_p(values), _p(out), values.size)
+    return out
+
+
+def bf16_decode(bits):
+    bits = _c(bits, np.uint16)
+    out = np.empty(bits.shape, dtype=np.float32)
+    LIB.oracle_bf16_decode(_p(bits), _p(out), bits.size)
+    return out
+
+
+def expf(x):
+    return LIB.oracle_expf(float(x))
+
+
+def e4m3_encode(value):
+    return LIB.oracle_e4m3_from_f32(float(value))
+
+
+def e4m3_decode(code):
+    return LIB.oracle_f32_from_e4m3(int(code))
+
+
+def e4m3_decode_array(codes):
+    table = np.array([LIB.oracle_f32_from_e4m3(c) for c in range(256)], dtype=np.float32)
+    return table[np.asarray(codes, dtype=np.uint8)]
+
+
+def sequence(count, seed):
+    out = np.empty(count, dtype=np.float32)
+    LIB.oracle_sequence(count, seed, _p(out))
+    return out
+
+
+def normal(count, seed, stddev=1.0, mean=0.0):
+    out = np.empty(count, dtype=np.float32)
+    LIB.oracle_normal(count, seed, mean, stddev, _p(out))
+    return out
+
+
+def max_tiles(tokens, top, local_experts, tile=128):
+    return LIB.oracle_max_tiles(tokens, top, local_experts, tile)
+
+
+def topk_softmax(scores, top, renormalize=True, score_kind=None, scale=None, scale_kind=-1,
+                 mapping=None, live=None, load=None, experts=None, rows=None):
+    """``scores``: float32/float16 array, or uint16 bf16 bits with score_kind=1."""
+    scores = np.ascontiguousarray(scores)
+    if score_kind is None:
+        score_kind = KINDS[scores.dtype]
+    rows = scores.shape[0] if rows is None else rows
+    experts = scores.shape[1] if experts is None else experts
+    ids = np.empty((rows, top), dtype=np.int32)
+    weights = np.empty((rows, top), dtype=np.float32)
+    live_arr = None if live is None else np.array([live], dtype=np.int32)
+    LIB.oracle_topk_softmax(_p(scores), score_kind, scores.shape[1], rows, experts, top,
+                            1 if renormalize else 0, _p(scale), scale_kind, _p(ids), _p(weights),
+                            _p(None if mapping is None else _c(mapping, np.int32)), _p(live_arr), _p(load))
+    return ids, weights
+
+
+def moe_sort(ids, local_experts, local_offset=0, live=None, tile=128, fill=-7):
+    """Device semantics: entries the sort does not write keep ``fill``."""
+    ids = _c(ids, np.int32)
+    tokens, top = ids.shape
+    tiles = max_tiles(tokens, top, local_experts, tile)
+    rows = max(tiles * tile, 1)
+    out = {
+        "tile_to_expert": np.full(max(tiles, 1), fill, np.int32),
+        "tile_to_limit": np.full(max(tiles, 1), fill, np.int32),
+        "expanded_to_permuted": np.full(max(tokens * top, 1), fill, np.int32),
+        "permuted_to_expanded": np.full(rows, fill, np.int32),
+        "permuted_to_token": np.full(rows, fill, np.int32),
+        "total_padded_tokens": np.full(1, fill, np.int32),
+        "num_non_exiting_tiles": np.full(1, fill, np.int32),
+    }
+    live_arr = None if live is None else np.array([live], dtype=np.int32)
+    LIB.oracle_moe_sort(_p(ids), tokens, top, local_experts, local_offset, tile, _p(live_arr),
+                        _p(out["tile_to_expert"]), _p(out["tile_to_limit"]),
+                        _p(out["expanded_to_permuted"]), _p(out["permuted_to_expanded"]),
+                        _p(out["permuted_to_token"]), _p(out["total_padded_tokens"]),
+                        _p(out["num_non_exiting_tiles"]))
+    return out
+
+
+def router_gemm(x_bits, w_bits):
+    x_bits, w_bits = _c(x_bits, np.uint16), _c(w_bits, np.uint16)
+    m, k = x_bits.shape
+    n = w_bits.shape[0]
+    out = np.empty((m, n), dtype=np.uint16)
+    LIB.oracle_router_gemm(_p(x_bits), _p(w_bits), m, n, k, _p(out))
+    return out
+
+
+def gather_gemm(hidden_bits, weight_bits, top, sort, rows, fill=np.nan):
+    hidden_bits, weight_bits = _c(hidden_bits, np.uint16), _c(weight_bits, np.uint16)
+    tokens, hidden = hidden_bits.shape
+    intermediate = weight_bits.shape[1] // 2
+    out = np.full((rows, intermediate), fill, dtype=np.float32)
+    LIB.oracle_gather_gemm(_p(hidden_bits), _p(weight_bits), tokens, hidden, intermediate, top, 128,
+                           _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
+                           _p(sort["permuted_to_expanded"]), int(sort["num_non_exiting_tiles"][0]), _p(out))
+    return out
+
+
+def route_gemm(rows_bits, weight_bits, sort, fill=np.nan):
+    rows_bits, weight_bits = _c(rows_bits, np.uint16), _c(weight_bits, np.uint16)
+    rows, intermediate = rows_bits.shape
+    hidden = weight_bits.shape[1]
+    out = np.full((rows, hidden), fill, dtype=np.float32)
+    LIB.oracle_route_gemm(_p(rows_bits), _p(weight_bits), hidden, intermediate, 128,
+                          _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
+                          int(sort["num_non_exiting_tiles"][0]), _p(out))
+    return out
+
+
+def moe_unpermute(routes_bits, expanded_to_permuted, scales, layout=0):
+    routes_bits = _c(routes_bits, np.uint16)
+    e2p = _c(expanded_to_permuted, np.int32)
+    scales = _c(scales, np.float32)
+    tokens, top = scales.shape
+    rows, hidden = routes_bits.shape
+    out = np.empty((tokens, hidden), dtype=np.float32)
+    LIB.oracle_moe_unpermute(_p(routes_bits), _p(e2p), _p(scales), tokens, top, hidden, rows, layout, _p(out))
+    return out
+
+
+def quantize_rows_fp8(bits, group=128):
+    bits = _c(bits, np.uint16)
+    rows, width = bits.shape
+    out = np.empty((rows, width), dtype=np.uint8)
+    scales = np.empty((rows, width // group), dtype=np.float32)
+    LIB.oracle_quantize_rows_fp8(_p(bits), rows, width, group, _p(out), _p(scales))
+    return out, scales
+
+
+def quantize_blocks_fp8(bits, block=128):
+    bits = _c(bits, np.uint16)
+    stacks, n, k = bits.shape
+    out = np.empty((stacks, n, k), dtype=np.uint8)
+    scales = np.empty((stacks, n // block, k // block), dtype=np.float32)
+    LIB.oracle_quantize_blocks_fp8(_p(bits), stacks, n, k, block, _p(out), _p(scales))
+    return out, scales
+
+
+def gather_gemm_fp8(hq, hs, wq, ws, top, sort, rows, fill=np.nan):
+    tokens, hidden = hq.shape
+    intermediate = wq.shape[1] // 2
+    out = np.full((rows, intermediate), fill, dtype=np.float32)
+    LIB.oracle_gather_gemm_fp8(_p(_c(hq, np.uint8)), _p(_c(hs, np.float32)), _p(_c(wq, np.uint8)),
+                               _p(_c(ws, np.float32)), tokens, hidden, intermediate, top, 128,
+                               _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
+                               _p(sort["permuted_to_expanded"]), int(sort["num_non_exiting_tiles"][0]), _p(out))
+    return out
+
+
+def route_gemm_fp8(gq, gs, wq, ws, sort, fill=np.nan):
+    rows, intermediate = gq.shape
+    hidden = wq.shape[1]
+    out = np.full((rows, hidden), fill, dtype=np.float32)
+    LIB.oracle_route_gemm_fp8(_p(_c(gq, np.uint8)), _p(_c(gs, np.float32)), _p(_c(wq, np.uint8)),
+                              _p(_c(ws, np.float32)), hidden, intermediate, 128,
+                              _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
+                              int(sort["num_non_exiting_tiles"][0]), _p(out))
+    return out
+
+
+def moe_layer(hidden_bits, router_bits, up_gate, down, top, renormalize=True, up_gate_scales=None,
+              down_scales=None):
+    """The composed layer on the CPU; answers (out bf16 bits, ids, weights, threads)."""
+    hidden_bits, router_bits = _c(hidden_bits, np.uint16), _c(router_bits, np.uint16)
+    tokens, hidden = hidden_bits.shape
+    experts = router_bits.shape[0]
+    intermediate = up_gate.shape[1] // 2
+    fp8 = up_gate.dtype == np.uint8
+    out = np.empty((tokens, hidden), dtype=np.uint16)
+    ids = np.empty((tokens, top), dtype=np.int32)
+    weights = np.empty((tokens, top), dtype=np.float32)
+    threads = LIB.oracle_moe_layer(_p(hidden_bits), _p(router_bits), _p(np.ascontiguousarray(up_gate)),
+                                   _p(up_gate_scales), _p(np.ascontiguousarray(down)), _p(down_scales),
+                                   tokens, hidden, experts, top, intermediate, 1 if renormalize else 0,
+                                   6 if fp8 else 4, _p(out), _p(ids), _p(weights))
+    return out, ids, weights, threads

@@ -1,0 +1,175 @@
+"""The C ABI without a GPU: layouts, exports and refusals.
+
+* every size and offset a header of ``include/`` asserts is the ctypes mirror's (the
+  reference's kernel checks assert the same against its generated headers,
+  tests/python/kernels/moe/test_moe_sort.py:87-89);
+* the shared object exports every entry the headers declare, and the router's code object
+  holds the kernel by its reference name;
+* the entries refuse what the reference's entries refuse, with a message in the call's error
+  buffer and a nonzero status, before anything is launched
+  (crates/ops/kernels/moe_sort/trtllm/src/entry.cpp:26-70, gather_gemm/cute_dsl/src/entry.cpp:18-42,
+  moe_unpermute/trtllm/src/entry.cpp:76-107, crates/ops/src/moe/routing.rs:127-238).
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from uniserve_moe import abi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+MIRRORS = {
+    "uniserve_moe_sort_call": abi.SortCall,
+    "uniserve_gather_call": abi.GatherCall,
+    "uniserve_route_call": abi.RouteCall,
+    "uniserve_unpermute_call": abi.UnpermuteCall,
+    "UniserveGemmCall": abi.GemmCall,
+}
+
+
+def asserted_layouts():
+    sizes, offsets = {}, {}
+    for header in HEADERS:
+        text = header.read_text()
+        for name, size in re.findall(r"static_assert\(sizeof\((\w+)\) == (\d+)", text):
+            sizes[name] = int(size)
+        for name, field, offset in re.findall(r"static_assert\(offsetof\((\w+), (\w+)\) == (\d+)", text):
+            offsets.setdefault(name, {})[field] = int(offset)
+    return sizes, offsets
+
+
+def test_every_asserted_layout_is_the_mirror_s():
+    sizes, offsets = asserted_layouts()
+    assert set(sizes) == set(MIRRORS)
+    for name, mirror in MIRRORS.items():
+        assert ctypes.sizeof(mirror) == sizes[name], name
+        fields = {f[0] for f in mirror._fields_}
+        assert set(offsets[name]) == fields, name
+        for field, offset in offsets[name].items():
+            assert getattr(mirror, field).offset == offset, (name, field)
+
+
+def test_reference_layout_sizes():
+    # The sizes the reference's generated headers assert (SURVEY: 648 / 632 / 616 / 608 / 600).
+    assert ctypes.sizeof(abi.SortCall) == 648
+    assert ctypes.sizeof(abi.GatherCall) == 632
+    assert ctypes.sizeof(abi.RouteCall) == 616
+    assert ctypes.sizeof(abi.UnpermuteCall) == 608
+    assert ctypes.sizeof(abi.GemmCall) == 600
+
+
+def declared_entries():
+    names = set()
+    for header in HEADERS:
+        text = header.read_text()
+        names.update(re.findall(r"UNISERVE_EXTERN_C\s+[\w\s\*]+?\b(uniserve_\w+)\s*\(", text))
+    return names
+
+
+def test_the_library_exports_every_declared_entry():
+    lib = abi.library()
+    names = declared_entries()
+    assert {"uniserve_moe_sort", "uniserve_gather_gemm", "uniserve_route_gemm", "uniserve_moe_unpermute",
+            "uniserve_gemm", "uniserve_topk_softmax_launch", "uniserve_moe_layer"} <= names
+    for name in sorted(names):
+        assert hasattr(lib, name), name
+    # The router kernel, by the name the reference's operator launches.
+    assert hasattr(lib, "uniserve_topk_softmax")
+    assert b"uniserve_topk_softmax" in abi.code_object_path().read_bytes()
+
+
+def message(call):
+    return bytes(call.error).split(b"\0", 1)[0].decode()
+
+
+def test_sort_refusals():
+    lib = abi.library()
+    call = abi.SortCall()
+    assert lib.uniserve_moe_sort(ctypes.byref(call), None) != 0
+    assert "seven metadata buffers" in message(call)
+    buffers = (ctypes.c_int32 * 4096)()
+    for name in ("ids", "tile_to_expert", "tile_to_limit", "expanded_to_permuted", "permuted_to_expanded",
+                 "permuted_to_token", "total_padded_tokens", "num_non_exiting_tiles"):
+        setattr(call, name, ctypes.addressof(buffers))
+    call.tokens, call.top, call.experts, call.local_experts, call.tile_tokens = 4, 2, 8, 8, 128
+    call.scales_dtype = abi.DTYPE["i32"]
+    assert lib.uniserve_moe_sort(ctypes.byref(call), None) != 0
+    assert "route weights" in message(call)
+    call.scales_dtype = abi.DTYPE["f32"]
+    call.local_offset = 4
+    assert lib.uniserve_moe_sort(ctypes.byref(call), None) != 0
+    assert "window" in message(call)
+    call.local_offset, call.local_experts, call.experts = 0, 1 << 20, 1 << 20
+    assert lib.uniserve_moe_sort(ctypes.byref(call), None) != 0
+    assert "LDS" in message(call)
+    assert lib.uniserve_moe_sort(None, None) != 0
+
+
+def test_product_refusals():
+    lib = abi.library()
+    g = abi.GatherCall()
+    g.dtype = abi.DTYPE["f16"]
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "bf16 only" in message(g)
+    g.dtype = abi.DTYPE["bf16"]
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "needs hidden" in message(g)
+    buf = (ctypes.c_uint8 * 64)()
+    for name in ("hidden", "weights", "out", "tile_to_expert", "tile_to_limit", "permuted_to_expanded",
+                 "num_non_exiting_tiles"):
+        setattr(g, name, ctypes.addressof(buf))
+    g.width, g.hidden_size, g.multiprocessors, g.tokens, g.top, g.experts = 3, 2048, 256, 4, 2, 8
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "even" in message(g)
+    g.width = 1536
+    g.multiprocessors = 0
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "multiprocessor" in message(g)
+    g.multiprocessors = 256
+    g.permuted_rows = 4
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "cannot hold" in message(g)
+
+    r = abi.RouteCall()
+    r.dtype = abi.DTYPE["f32"]
+    assert lib.uniserve_route_gemm(ctypes.byref(r), None) != 0 and "bf16 only" in message(r)
+
+    u = abi.UnpermuteCall()
+    u.input_dtype, u.output_dtype = abi.DTYPE["bf16"], abi.DTYPE["f32"]
+    assert lib.uniserve_moe_unpermute(ctypes.byref(u), None) != 0 and "one input and output" in message(u)
+    u.output_dtype = abi.DTYPE["bf16"]
+    for name in ("routes", "out", "expanded_to_permuted", "scales"):
+        setattr(u, name, ctypes.addressof(buf))
+    u.hidden, u.top, u.tokens = 12, 2, 1
+    assert lib.uniserve_moe_unpermute(ctypes.byref(u), None) != 0 and "8-element" in message(u)
+
+    q = abi.GemmCall()
+    assert lib.uniserve_gemm(ctypes.byref(q), None) != 0 and "needs out" in message(q)
+
+
+def test_router_refusals():
+    lib = abi.library()
+    error = ctypes.create_string_buffer(512)
+    buf = (ctypes.c_uint8 * 64)()
+    p = ctypes.addressof(buf)
+
+    def launch(kind=1, experts=128, top=8, rows=4, stride=128, scale_kind=-1):
+        return lib.uniserve_topk_softmax_launch(p, kind, stride, rows, experts, top, 1, None, scale_kind,
+                                                p, p, None, None, None, None, error, 512)
+
+    assert launch(kind=7) != 0 and b"routeable" in error.value
+    assert launch(experts=0) != 0 and b"at least one expert" in error.value
+    assert launch(top=9, experts=8, stride=8) != 0 and b"outside" in error.value
+    assert launch(experts=2048, stride=2048) != 0 and b"1024" in error.value
+    assert launch(top=33, experts=64, stride=64) != 0 and b"32 picks" in error.value
+    assert launch(stride=64) != 0 and b"overlap" in error.value
+    assert launch(scale_kind=0) != 0 and b"scale" in error.value
+    assert launch(rows=0) == 0  # nothing to route launches nothing
+
+
+def test_layer_workspace_and_refusals():
+    lib = abi.library()
+    assert lib.uniserve_moe_max_tiles(64, 8, 128, 128) == 131
+    assert lib.uniserve_moe_layer_workspace(64, 2048, 128, 8, 768, abi.DTYPE["bf16"]) > 0
+    assert lib.uniserve_moe_layer_workspace(64, 2048, 128, 8, 768, abi.DTYPE["f16"]) == -1
+    call = abi.LayerCall()
+    assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "needs hidden" in message(call)

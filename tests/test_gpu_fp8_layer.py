@@ -1,0 +1,228 @@
+"""The block-scaled e4m3 path and the composed layer on the MI355X against the oracle.
+
+* the activation quantiser writes the oracle's codes and scales bit for bit;
+* the e4m3 products agree with the oracle's FP32 evaluation over dequantised values within
+  BASELINE's fp8 bar (4e-2 of the peak) - the format has no reference counterpart, so this is
+  parity with the oracle's definition, unpinned against the reference;
+* the whole layer (router gemm -> topk -> sort -> FC1 -> FC2 -> combine) agrees with the
+  oracle's composition: router ids bit-exact, outputs within the bf16 / fp8 bars; at prefill
+  size the oracle evaluates a sample of tokens (the layer is per token, so any subset of rows
+  is its own smaller call);
+* a captured HIP graph of the layer replays to the eager result, bit for bit, across replays
+  with eager work between them.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from gpu_helpers import announce, assert_bf16_bar, bf16_bits, bf16_values, normal_bf16, sort_on_host, zipf_bias
+from uniserve_moe import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def test_quantiser_is_bit_exact(device):
+    announce("quantize fp8")
+    x = normal_bf16((333, 2048), 8, device=device)
+    x[5] = 0
+    x[6, :128] = 1e-30
+    q, s = ops.quantize_fp8(x)
+    torch.cuda.synchronize()
+    want_q, want_s = O.quantize_rows_fp8(bf16_bits(x))
+    np.testing.assert_array_equal(q.cpu().numpy(), want_q)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+    limit = torch.tensor([100], dtype=torch.int32, device=device)
+    q2 = torch.full((333, 2048), 0xAB, dtype=torch.uint8, device=device)
+    s2 = torch.full((333, 16), -1.0, device=device)
+    call_q, call_s = ops.quantize_fp8(x[:200].contiguous(), row_limit=limit)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(call_q[:100].cpu().numpy(), want_q[:100])
+    del q2, s2
+
+
+def quantized_stacks(device, experts, hidden, intermediate, seed=2):
+    up_gate = normal_bf16((experts, 2 * intermediate, hidden), seed, 0.02, device)
+    down = normal_bf16((experts, hidden, intermediate), seed + 1, 0.02, device)
+    q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+    q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+    return q1, s1, q2, s2
+
+
+@pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew", [
+    (64, 2048, 128, 8, 768, "uniform"), (1024, 2048, 128, 8, 768, "zipf"), (5, 4096, 16, 8, 1536, "uniform")])
+def test_fp8_products(device, tokens, hidden, experts, top, intermediate, skew):
+    announce("fp8 products", tokens, hidden, experts, top, intermediate, skew)
+    rng = np.random.default_rng(tokens)
+    if skew == "zipf":
+        p = np.exp(zipf_bias(experts).astype(np.float64))
+        ids_host = np.stack([rng.choice(experts, size=top, replace=False, p=p / p.sum()) for _ in range(tokens)])
+    else:
+        ids_host = np.stack([rng.choice(experts, size=top, replace=False) for _ in range(tokens)])
+    q1, s1, q2, s2 = quantized_stacks(device, experts, hidden, intermediate)
+    x = normal_bf16((tokens, hidden), 1, device=device)
+    xq, xs = ops.quantize_fp8(x)
+    ids = torch.from_numpy(ids_host.astype(np.int32)).to(device)
+    weights = torch.rand((tokens, top), device=device)
+    maps = ops.moe_sort(ids, weights, experts)
+    rows = ops.permuted_rows(tokens, top, experts)
+    d = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    gated = torch.full((rows, intermediate), float("nan"), dtype=torch.bfloat16, device=device)
+    ops.gather_gemm_fp8(xq, xs, d(q1), d(s1), top, maps, rows, out=gated)
+    padded_t = maps[ops.TOTAL_PADDED_TOKENS][:1]
+    gq, gs = ops.quantize_fp8(torch.nan_to_num(gated, 0.0), row_limit=padded_t)
+    products = torch.full((rows, hidden), float("nan"), dtype=torch.bfloat16, device=device)
+    ops.route_gemm_fp8(gq, gs, d(q2), d(s2), maps, out=products)
+    torch.cuda.synchronize()
+
+    sort = sort_on_host(maps, tokens, top)
+    padded = int(sort["total_padded_tokens"][0])
+    live = sort["permuted_to_expanded"][:padded] >= 0
+    want_gated = O.gather_gemm_fp8(xq.cpu().numpy(), xs.cpu().numpy(), q1, s1, top, sort, rows)
+    got_gated = bf16_values(gated)
+    assert_bf16_bar(got_gated[:padded][live], want_gated[:padded][live], "gather_gemm_fp8", max_rel=4e-2)
+    assert np.isnan(got_gated[:padded][~live]).all()
+    want_products = O.route_gemm_fp8(gq.cpu().numpy()[:padded], gs.cpu().numpy()[:padded], q2, s2, sort)
+    got_products = bf16_values(products)
+    assert_bf16_bar(got_products[:padded][live], want_products[:padded][live], "route_gemm_fp8", max_rel=4e-2)
+
+
+LAYERS = {
+    # name: tokens, hidden, experts, top, intermediate, weights, zipf, oracle sample
+    "tiny (configs[0] shape, bf16)": (16, 256, 8, 2, 128, "bf16", False, None),
+    "30b decode bf16": (64, 2048, 128, 8, 768, "bf16", False, None),
+    "30b prefill bf16 zipf": (8192, 2048, 128, 8, 768, "bf16", True, 96),
+    "30b decode fp8": (64, 2048, 128, 8, 768, "f8e4m3", False, None),
+    "30b prefill fp8 zipf": (8192, 2048, 128, 8, 768, "f8e4m3", True, 96),
+    "235b decode fp8 one token": (1, 4096, 128, 8, 1536, "f8e4m3", False, None),
+}
+
+
+def layer_inputs(device, tokens, hidden, experts, intermediate, seed=0):
+    x = normal_bf16((tokens, hidden), seed + 1, device=device)
+    router = normal_bf16((experts, hidden), seed + 2, 0.02, device)
+    up_gate = normal_bf16((experts, 2 * intermediate, hidden), seed + 3, 0.02, device)
+    down = normal_bf16((experts, hidden, intermediate), seed + 4, 0.02, device)
+    return x, router, up_gate, down
+
+
+@pytest.mark.parametrize("case", list(LAYERS))
+def test_layer_against_the_oracle(device, case):
+    tokens, hidden, experts, top, intermediate, wdtype, zipf, sample = LAYERS[case]
+    announce("layer", case)
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate)
+    bias = torch.from_numpy(zipf_bias(experts)).to(device) if zipf else None
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+    args = {}
+    if wdtype == "f8e4m3":
+        q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+        up_gate_dev, down_dev = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+        args = dict(up_gate_scales=torch.from_numpy(s1).to(device), down_scales=torch.from_numpy(s2).to(device))
+        host_w = (q1, q2, s1, s2)
+    else:
+        up_gate_dev, down_dev = up_gate, down
+        host_w = (bf16_bits(up_gate), bf16_bits(down), None, None)
+    out = layer(x, router, up_gate_dev, down_dev, router_bias=bias, **args)
+    torch.cuda.synchronize()
+    ids = layer.view("ids", torch.int32, (tokens, top)).cpu().numpy()
+    got = bf16_values(out)
+    assert np.isfinite(got).all()
+
+    rows = np.arange(tokens) if sample is None else np.random.default_rng(0).choice(tokens, sample, replace=False)
+    x_bits = bf16_bits(x)[rows]
+    router_bits = bf16_bits(router)
+    if zipf:
+        # The bias enters the scores before their rounding; the oracle's router has no bias, so it
+        # is handed the device's own bf16 scores through a router of one-hot rows.
+        scores = layer.view("scores", torch.bfloat16, (tokens, experts))
+        want_ids, _ = O.topk_softmax(bf16_bits(scores)[rows], top, score_kind=1)
+        np.testing.assert_array_equal(ids[rows], want_ids)
+        hist = np.bincount(ids.ravel(), minlength=experts)
+        assert hist[0] > 3 * hist[experts // 2], "the Zipf bias skews the routing"
+        # Products and combine of the sampled tokens, from the device's routing.
+        want = sampled_layer(x_bits, ids[rows], layer.view("weights", torch.float32, (tokens, top)).cpu().numpy()[rows],
+                             host_w, experts, top)
+    else:
+        want_bits, want_ids, want_weights, _ = O.moe_layer(
+            x_bits, router_bits, host_w[0], host_w[1], top, up_gate_scales=host_w[2], down_scales=host_w[3])
+        np.testing.assert_array_equal(ids[rows], want_ids)
+        want = O.bf16_decode(want_bits).astype(np.float64)
+    bar = 4e-2 if wdtype == "f8e4m3" else 2e-2
+    assert_bf16_bar(got[rows], want, case, max_rel=bar)
+
+
+def sampled_layer(x_bits, ids, weights, host_w, experts, top):
+    """The oracle's products and combine for a sample of tokens with given routes."""
+    tokens = x_bits.shape[0]
+    w1, w2, s1, s2 = host_w
+    sort = O.moe_sort(ids, experts)
+    rows = O.max_tiles(tokens, top, experts) * 128
+    padded = int(sort["total_padded_tokens"][0])
+    if s1 is not None:
+        xq, xs = O.quantize_rows_fp8(x_bits)
+        gated = O.gather_gemm_fp8(xq, xs, w1, s1, top, sort, rows, fill=0.0)
+        gq, gs = O.quantize_rows_fp8(O.bf16_encode(gated))
+        products = O.route_gemm_fp8(gq, gs, w2, s2, sort, fill=0.0)
+    else:
+        gated = O.gather_gemm(x_bits, w1, top, sort, rows, fill=0.0)
+        products = O.route_gemm(O.bf16_encode(gated), w2, sort, fill=0.0)
+    del padded
+    combined = O.moe_unpermute(O.bf16_encode(products), sort["expanded_to_permuted"][: tokens * top].reshape(tokens, top), weights)
+    return O.bf16_decode(O.bf16_encode(combined)).astype(np.float64)
+
+
+def test_layer_live_tokens_leave_padding_rows_zero(device):
+    announce("layer live tokens")
+    tokens, hidden, experts, top, intermediate = 64, 2048, 128, 8, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 10)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens)
+    full = layer(x, router, up_gate, down).clone()
+    live = torch.tensor([40], dtype=torch.int32, device=device)
+    part = layer(x, router, up_gate, down, live_tokens=live)
+    torch.cuda.synchronize()
+    assert (bf16_values(part)[40:] == 0).all()
+    np.testing.assert_array_equal(bf16_bits(part)[:40], bf16_bits(full)[:40])
+
+
+@pytest.mark.parametrize("wdtype", ["bf16", "f8e4m3"])
+def test_layer_graph_replays_match_eager(device, wdtype):
+    announce("layer graph", wdtype)
+    tokens, hidden, experts, top, intermediate = 64, 2048, 128, 8, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 20)
+    args = {}
+    if wdtype == "f8e4m3":
+        q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+        up_gate, down = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+        args = dict(up_gate_scales=torch.from_numpy(s1).to(device), down_scales=torch.from_numpy(s2).to(device))
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=device)
+    layer(x, router, up_gate, down, out=out, **args)
+    torch.cuda.synchronize()
+    eager = bf16_bits(out).copy()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            layer(x, router, up_gate, down, out=out, **args)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        out.zero_()
+        _ = torch.randn(1000, device=device).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bf16_bits(out), eager, err_msg=f"replay {replay}")
+
+
+def test_layer_is_deterministic(device):
+    announce("layer determinism")
+    tokens, hidden, experts, top, intermediate = 2048, 2048, 128, 8, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 30)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens)
+    a = bf16_bits(layer(x, router, up_gate, down)).copy()
+    b = bf16_bits(layer(x, router, up_gate, down))
+    np.testing.assert_array_equal(a, b)

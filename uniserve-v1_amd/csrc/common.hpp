@@ -1,0 +1,124 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// Pieces every kernel file of the MI355X (gfx950) MoE library shares: element conversions, the
+// MFMA operand types, wave64 helpers and the refusal convention of the C entries.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <exception>
+
+#include "uniserve_abi.h"
+
+namespace uniserve {
+
+constexpr int kWave = 64;
+
+// ---- refusals ------------------------------------------------------------------------------------
+
+/// Writes a NUL-terminated message into `error` (512 bytes) and answers 1: the entries' way of
+/// refusing a call (crates/ops/src/abi.rs:58-70, crates/ops/src/kernel.rs:17-29).
+inline int32_t refuse_into(char *error, const char *format, ...) {
+  if (error != nullptr) {
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(error, 512, format, args);
+    va_end(args);
+  }
+  return 1;
+}
+
+#define UNISERVE_REFUSE(call, ...) ::uniserve::refuse_into(const_cast<char *>((call)->error), __VA_ARGS__)
+
+/// Runs `body` (which answers an int32 status) and turns any exception into a refusal, so nothing
+/// unwinds across the C boundary (the reference's entries do the same:
+/// crates/ops/kernels/moe_sort/trtllm/src/entry.cpp:73-91).
+template <class Call, class Body>
+int32_t guarded(const Call *call, Body body) {
+  if (call == nullptr) return 1;
+  try {
+    return body();
+  } catch (std::exception const &thrown) {
+    return UNISERVE_REFUSE(call, "%s", thrown.what());
+  } catch (...) {
+    return UNISERVE_REFUSE(call, "the launch failed without stating why");
+  }
+}
+
+/// The status of the launch just issued: 0, or a refusal naming the runtime's error.
+template <class Call>
+int32_t launched(const Call *call, const char *what) {
+  const hipError_t status = hipGetLastError();
+  if (status == hipSuccess) return 0;
+  return UNISERVE_REFUSE(call, "%s could not start: %s", what, hipGetErrorString(status));
+}
+
+// ---- element conversions ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t bits) {
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+/// Round to nearest even into bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float value) {
+  uint32_t bits = __float_as_uint(value);
+  if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x40u);
+  bits += 0x7fffu + ((bits >> 16) & 1u);
+  return static_cast<uint16_t>(bits >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+/// silu(g) = g / (1 + e^-g), with the hardware exponential (v_exp_f32 on g * -log2 e).
+__device__ __forceinline__ float silu(float g) {
+  return g / (1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
+// ---- MFMA operands ------------------------------------------------------------------------------------
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef int intx8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+/// D = A . B + C over a 16 x 16 x 32 bf16 block: lane l supplies A row l % 16 and B column
+/// l % 16, eight K elements each; D row 4 (l / 16) + i, column l % 16 lands in element i.
+__device__ __forceinline__ floatx4 mfma_16x16x32_bf16(u32x4 a, u32x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+/// The same block shape over 128 K elements of OCP e4m3 (32 per lane), unscaled.
+__device__ __forceinline__ floatx4 mfma_16x16x128_fp8(intx8 a, intx8 b, floatx4 c) {
+  // cbsz/blgp 0 = e4m3 for both operands; scale exponents 127 = 2^0.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ---- wave64 helpers --------------------------------------------------------------------------------------
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ uint64_t ballot(bool predicate) { return __ballot(predicate); }
+
+/// The lanes of the wave whose `key` equals this lane's, for keys below 2^bits.
+__device__ __forceinline__ uint64_t match_any(uint32_t key, int bits) {
+  uint64_t peers = ~0ull;
+  for (int bit = 0; bit < bits; ++bit) {
+    const bool set = (key >> bit) & 1u;
+    const uint64_t mask = ballot(set);
+    peers &= set ? mask : ~mask;
+  }
+  return peers;
+}
+
+template <class T>
+__host__ __device__ constexpr T ceil_div(T a, T b) {
+  return (a + b - 1) / b;
+}
+
+}  // namespace uniserve

@@ -1,0 +1,410 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The two grouped expert products in bf16 on gfx950 MFMA (operators: crates/ops/src/moe/grouped.rs;
+// reference packages: crates/ops/kernels/{gather_gemm,route_gemm}/cute_dsl):
+//
+//   gather_gemm (FC1)  out[p, :I] = silu(W[e, I:2I] . x[t]) * (W[e, :I] . x[t])
+//   route_gemm  (FC2)  out[p, :H] = W[e] . rows[p]
+//
+// for every live permuted row p (below its tile's `tile_to_limit`) of every tile below
+// `num_non_exiting_tiles`, e = tile_to_expert[tile], t = permuted_to_expanded[p] / top. FP32
+// accumulation, the activation on the accumulators, one rounding into bf16; rows past a tile's
+// limit are neither read nor stored.
+//
+// Two kernels per product, chosen on the host from the expected rows per expert (tokens x top /
+// experts), which is all the host knows without reading device memory:
+//
+//  * `stream` (decode: a few rows per expert). Weight-streaming bound: every touched expert's
+//    matrix is read once from HBM and nothing else matters. A workgroup owns one tile and a
+//    128-row slice of the expert's weight rows; each wavefront streams 32 weight rows straight from
+//    HBM into registers (64 contiguous bytes per lane per row, double-buffered, no LDS), and the
+//    tile's activation rows come from L2. The weight rows are MFMA operand A and the activation
+//    rows operand B (16x16x32 bf16), so each lane ends holding four consecutive output columns of
+//    one row - an 8-byte store - and the SiLU pair (up column n, gate column n) meets in one lane.
+//    Tiles of more than 32 rows are covered in passes of 32.
+//
+//  * `tiled` (prefill: hundreds of rows per expert). MFMA-bound: a 128 x 128 output tile per
+//    workgroup, 64-deep K steps staged through XOR-swizzled LDS (two stages, one barrier per step),
+//    four wavefronts of 64 x 64, global loads of step k + 1 in flight during the MFMAs of step k.
+//
+// The dot products over K use a permutation of K that both operands share (lane group g of a
+// 128-element chunk holds elements 32g..32g+31), which changes only the FP32 summation order.
+#include "common.hpp"
+#include "uniserve_gather_gemm.h"
+#include "uniserve_route_gemm.h"
+
+namespace uniserve {
+namespace {
+
+constexpr int kTileRows = 128;
+constexpr int kThreads = 256;
+
+struct GroupedParams {
+  const uint16_t *act;      ///< FC1: hidden [tokens, K]; FC2: rows [permuted_rows, K]
+  const uint16_t *weights;  ///< [experts, n_total, K]
+  uint16_t *out;            ///< [permuted_rows, out_width]
+  const int32_t *tile_to_expert;
+  const int32_t *tile_to_limit;
+  const int32_t *permuted_to_expanded;
+  const int32_t *num_tiles;
+  int64_t K;
+  int64_t n_total;          ///< weight rows per expert: 2I (FC1) or H (FC2)
+  int64_t out_width;        ///< I (FC1) or H (FC2)
+  int64_t top;
+};
+
+__device__ __forceinline__ u32x4 load16(const uint16_t *pointer) {
+  return *reinterpret_cast<const u32x4 *>(pointer);
+}
+
+__device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
+  uint2 packed;
+  packed.x = pack_bf16x2(v[0], v[1]);
+  packed.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2 *>(pointer) = packed;
+}
+
+// ---- stream kernel -----------------------------------------------------------------------------------
+
+/// Rows of a tile one pass covers: kPassTiles MFMA blocks of 16.
+constexpr int kPassTiles = 2;
+
+template <bool kGated>
+struct StreamChunk {
+  u32x4 w[2][4];             ///< [row set][MFMA K step]
+  u32x4 a[kPassTiles][4];    ///< [16-row block][MFMA K step]
+};
+
+template <bool kGated>
+__device__ __forceinline__ void stream_load(StreamChunk<kGated> &chunk, const uint16_t *w0,
+                                            const uint16_t *w1, const uint16_t *const *a,
+                                            const bool *valid, int64_t offset) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    chunk.w[0][j] = load16(w0 + offset + j * 8);
+    chunk.w[1][j] = load16(w1 + offset + j * 8);
+  }
+#pragma unroll
+  for (int ms = 0; ms < kPassTiles; ++ms)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) chunk.a[ms][j] = valid[ms] ? load16(a[ms] + offset + j * 8) : u32x4{0, 0, 0, 0};
+}
+
+template <bool kGated>
+__device__ __forceinline__ void stream_compute(const StreamChunk<kGated> &chunk,
+                                               floatx4 (&acc)[2][kPassTiles]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      acc[0][ms] = mfma_16x16x32_bf16(chunk.w[0][j], chunk.a[ms][j], acc[0][ms]);
+      acc[1][ms] = mfma_16x16x32_bf16(chunk.w[1][j], chunk.a[ms][j], acc[1][ms]);
+    }
+}
+
+/// Grid: (max tiles, weight-row slices). FC1 slices are 64 gated columns (64 up + 64 gate rows),
+/// FC2 slices 128 output columns; wavefront w takes 16 + 16 of them. Needs K % 128 == 0.
+template <bool kGated>
+__global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
+  const int tile = static_cast<int>(blockIdx.x);
+  if (tile >= p.num_tiles[0]) return;
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  int64_t n0, n1;
+  if constexpr (kGated) {
+    n0 = static_cast<int64_t>(blockIdx.y) * 64 + wave * 16;
+    n1 = p.out_width + n0;
+  } else {
+    n0 = static_cast<int64_t>(blockIdx.y) * 128 + wave * 32;
+    n1 = n0 + 16;
+    if (n0 >= p.out_width) return;  // a last slice of 64 columns leaves two wavefronts idle
+  }
+  const uint16_t *w0 = p.weights + (expert * p.n_total + n0 + r16) * p.K + g * 32;
+  const uint16_t *w1 = p.weights + (expert * p.n_total + n1 + r16) * p.K + g * 32;
+  const int chunks = static_cast<int>(p.K / 128);
+
+  for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
+    const uint16_t *a[kPassTiles];
+    bool valid[kPassTiles];
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      valid[ms] = m < rows;
+      int64_t source = first + m;
+      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      a[ms] = p.act + (valid[ms] ? source : 0) * p.K + g * 32;
+    }
+    floatx4 acc[2][kPassTiles];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    StreamChunk<kGated> even, odd;
+    stream_load(even, w0, w1, a, valid, 0);
+    for (int c = 0; c < chunks; c += 2) {
+      if (c + 1 < chunks) stream_load(odd, w0, w1, a, valid, static_cast<int64_t>(c + 1) * 128);
+      stream_compute(even, acc);
+      if (c + 2 < chunks) stream_load(even, w0, w1, a, valid, static_cast<int64_t>(c + 2) * 128);
+      if (c + 1 < chunks) stream_compute(odd, acc);
+    }
+
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      if (m >= rows) continue;
+      uint16_t *row = p.out + (first + m) * p.out_width;
+      if constexpr (kGated) {
+        floatx4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        store_bf16x4(row + n0 + 4 * g, h);
+      } else {
+        store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
+        store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
+      }
+    }
+  }
+}
+
+// ---- tiled kernel -----------------------------------------------------------------------------------------
+
+constexpr int kBK = 64;               // K elements per stage: 8 chunks of 16 bytes per row
+constexpr int kStageChunks = 128 * 8; // 16-byte chunks per operand per stage
+
+__device__ __forceinline__ int swizzled(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+/// Grid: (max tiles, weight-row slices of 128: FC1 64 up + 64 gate rows, FC2 128 rows).
+/// Needs K % 64 == 0.
+template <bool kGated>
+__global__ void __launch_bounds__(kThreads) tiled_kernel(GroupedParams p) {
+  __shared__ u32x4 shared_a[2][kStageChunks];
+  __shared__ u32x4 shared_w[2][kStageChunks];
+  const int tile = static_cast<int>(blockIdx.x);
+  if (tile >= p.num_tiles[0]) return;
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int t = static_cast<int>(threadIdx.x);
+  const int wave = t / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  const int64_t slice = static_cast<int64_t>(blockIdx.y) * (kGated ? 64 : 128);
+
+  // This thread's four rows of each operand and its 16-byte chunk within a stage.
+  const int chunk = t & 7;
+  const uint16_t *a_row[4];
+  const uint16_t *w_row[4];
+  bool a_valid[4], w_valid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (t >> 3) + 32 * i;
+    a_valid[i] = r < rows;
+    int64_t source = first + r;
+    if constexpr (kGated) source = a_valid[i] ? p.permuted_to_expanded[first + r] / p.top : 0;
+    a_row[i] = p.act + (a_valid[i] ? source : 0) * p.K + chunk * 8;
+    int64_t n;
+    if constexpr (kGated) n = r < 64 ? slice + r : p.out_width + slice + (r - 64);
+    else n = slice + r;
+    w_valid[i] = kGated ? true : n < p.out_width;
+    w_row[i] = p.weights + (expert * p.n_total + (w_valid[i] ? n : 0)) * p.K + chunk * 8;
+  }
+
+  u32x4 staged_a[4], staged_w[4];
+  auto fetch = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      staged_a[i] = a_valid[i] ? load16(a_row[i] + k0) : u32x4{0, 0, 0, 0};
+      staged_w[i] = w_valid[i] ? load16(w_row[i] + k0) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto deposit = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (t >> 3) + 32 * i;
+      shared_a[stage][swizzled(r, chunk)] = staged_a[i];
+      shared_w[stage][swizzled(r, chunk)] = staged_w[i];
+    }
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int steps = static_cast<int>(p.K / kBK);
+  fetch(0);
+  deposit(0);
+  __syncthreads();
+  for (int step = 0; step < steps; ++step) {
+    const int stage = step & 1;
+    if (step + 1 < steps) fetch(static_cast<int64_t>(step + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + g;
+      u32x4 wf[4], af[4];
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        int r;
+        if constexpr (kGated) r = (ni < 2 ? wn * 32 + ni * 16 : 64 + wn * 32 + (ni - 2) * 16) + r16;
+        else r = wn * 64 + ni * 16 + r16;
+        wf[ni] = shared_w[stage][swizzled(r, c)];
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int r = wm * 64 + mi * 16 + r16;
+        af[mi] = shared_a[stage][swizzled(r, c)];
+      }
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = mfma_16x16x32_bf16(wf[ni], af[mi], acc[ni][mi]);
+    }
+    if (step + 1 < steps) deposit(stage ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const int m = wm * 64 + mi * 16 + r16;
+    if (m >= rows) continue;
+    uint16_t *row = p.out + (first + m) * p.out_width;
+    if constexpr (kGated) {
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        floatx4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = silu(acc[ni + 2][mi][i]) * acc[ni][mi][i];
+        store_bf16x4(row + slice + wn * 32 + ni * 16 + 4 * g, h);
+      }
+    } else {
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        const int64_t col = slice + wn * 64 + ni * 16 + 4 * g;
+        if (col < p.out_width) store_bf16x4(row + col, acc[ni][mi]);
+      }
+    }
+  }
+}
+
+/// The stream kernel serves batches whose experts average fewer rows than this.
+constexpr int64_t kStreamRowsPerExpert = 24;
+
+template <bool kGated>
+void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, hipStream_t s) {
+  if (stream_path) {
+    const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
+    hipLaunchKernelGGL(stream_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
+                       dim3(kThreads), 0, s, p);
+  } else {
+    const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
+    hipLaunchKernelGGL(tiled_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
+                       dim3(kThreads), 0, s, p);
+  }
+}
+
+}  // namespace
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_gather_gemm(const uniserve_gather_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    // The refusals of the reference entry (gather_gemm/cute_dsl/src/entry.cpp:18-42) and of
+    // `GatherGemm::check` (crates/ops/src/moe/grouped.rs:250-324) the call's words can state.
+    if (call->dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm serves bf16 only");
+    if (call->hidden == nullptr || call->weights == nullptr || call->out == nullptr)
+      return UNISERVE_REFUSE(call, "gather_gemm needs hidden, weights and out");
+    if (call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->permuted_to_expanded == nullptr || call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "gather_gemm needs the sort's tile and route maps");
+    if (call->width % 2 != 0) return UNISERVE_REFUSE(call, "gather_gemm needs an even 2*intermediate width");
+    if (call->multiprocessors <= 0 || call->multiprocessors > INT32_MAX)
+      return UNISERVE_REFUSE(call, "gather_gemm needs its device's multiprocessor count");
+    if (call->hidden_size <= 0 || call->hidden_size % 64 != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm needs a hidden size of whole 64-element steps");
+    if (call->width <= 0 || (call->width / 2) % 64 != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm needs an intermediate width of whole 64-column blocks");
+    if (call->tokens < 0 || call->top <= 0 || call->experts <= 0)
+      return UNISERVE_REFUSE(call, "gather_gemm needs non-negative tokens and positive top and experts");
+    if (call->permuted_rows < call->tokens * call->top)
+      return UNISERVE_REFUSE(call, "%lld permuted rows cannot hold %lld routes",
+                             static_cast<long long>(call->permuted_rows),
+                             static_cast<long long>(call->tokens * call->top));
+    if (call->permuted_rows % kTileRows != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm needs permuted rows of whole 128-row tiles");
+    const int64_t max_tiles = call->permuted_rows / kTileRows;
+    if (max_tiles == 0) return 0;
+    if (max_tiles > 0x7fffffffLL) return UNISERVE_REFUSE(call, "gather_gemm: too many tiles for one grid");
+
+    GroupedParams p{};
+    p.act = static_cast<const uint16_t *>(call->hidden);
+    p.weights = static_cast<const uint16_t *>(call->weights);
+    p.out = static_cast<uint16_t *>(call->out);
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.num_tiles = call->num_non_exiting_tiles;
+    p.K = call->hidden_size;
+    p.n_total = call->width;
+    p.out_width = call->width / 2;
+    p.top = call->top;
+    const bool stream_path = call->tokens * call->top < kStreamRowsPerExpert * call->experts &&
+                             call->hidden_size % 128 == 0;
+    launch_grouped<true>(p, max_tiles, stream_path, static_cast<hipStream_t>(stream));
+    return launched(call, "gather_gemm");
+  });
+}
+
+extern "C" int32_t uniserve_route_gemm(const uniserve_route_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "route_gemm serves bf16 only");
+    if (call->rows == nullptr || call->weights == nullptr || call->out == nullptr)
+      return UNISERVE_REFUSE(call, "route_gemm needs rows, weights and out");
+    if (call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->permuted_to_expanded == nullptr || call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "route_gemm needs the sort's tile and route maps");
+    if (call->multiprocessors <= 0 || call->multiprocessors > INT32_MAX)
+      return UNISERVE_REFUSE(call, "route_gemm needs its device's multiprocessor count");
+    if (call->intermediate <= 0 || call->intermediate % 64 != 0)
+      return UNISERVE_REFUSE(call, "route_gemm needs an intermediate width of whole 64-element steps");
+    if (call->width <= 0 || call->width % 64 != 0)
+      return UNISERVE_REFUSE(call, "route_gemm needs a hidden width of whole 64-column blocks");
+    if (call->experts <= 0) return UNISERVE_REFUSE(call, "route_gemm needs positive experts");
+    if (call->permuted_rows < 0 || call->permuted_rows % kTileRows != 0)
+      return UNISERVE_REFUSE(call, "route_gemm needs permuted rows of whole 128-row tiles");
+    const int64_t max_tiles = call->permuted_rows / kTileRows;
+    if (max_tiles == 0) return 0;
+    if (max_tiles > 0x7fffffffLL) return UNISERVE_REFUSE(call, "route_gemm: too many tiles for one grid");
+
+    GroupedParams p{};
+    p.act = static_cast<const uint16_t *>(call->rows);
+    p.weights = static_cast<const uint16_t *>(call->weights);
+    p.out = static_cast<uint16_t *>(call->out);
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.num_tiles = call->num_non_exiting_tiles;
+    p.K = call->intermediate;
+    p.n_total = call->width;
+    p.out_width = call->width;
+    p.top = 1;
+    // The call states no token count: the permuted rows bound the routes, and their expected
+    // share per expert is (rows - the padding of one partial tile per expert) / experts.
+    const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
+    const bool stream_path = routes_bound < kStreamRowsPerExpert * call->experts &&
+                             call->intermediate % 128 == 0;
+    launch_grouped<false>(p, max_tiles, stream_path, static_cast<hipStream_t>(stream));
+    return launched(call, "route_gemm");
+  });
+}

@@ -1,0 +1,510 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// Block-scaled OCP e4m3 forms of the grouped expert products, and the activation quantiser they
+// read (no reference counterpart: crates/nn/src/quantization.rs:241-249 refuses 128x128
+// block-scaled checkpoints; this is the format BASELINE names, in the call style of the
+// reference's NVFP4 operators, crates/ops/src/moe/grouped.rs:816-869).
+//
+// Values are code * scale with one FP32 scale per 128 x 128 weight block and per 128 channels of an
+// activation row. One gfx950 MFMA 16x16x128 (f8f6f4, e4m3 x e4m3) spans exactly one scale block
+// along K, so each block's product is formed exactly as the hardware accumulates it and then added
+// into the FP32 accumulator times s_w * s_x - the per-block dequantisation never touches the
+// operands. The kernels mirror the bf16 ones (`stream` for decode, `tiled` for prefill); the
+// quantiser's codes are bit-exact with the host rule (nearest even, saturating at 448).
+#include "common.hpp"
+#include "grouped_fp8.hpp"
+#include "uniserve_moe_fp8.h"
+
+namespace uniserve {
+
+// ---- e4m3 encoding ---------------------------------------------------------------------------------------
+
+/// Nearest-even e4m3fn code of `value`, saturating at +-448 (0x7e); NaN -> 0x7f.
+__device__ __forceinline__ uint32_t e4m3_encode(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const float a = __builtin_fabsf(value);
+  if (a != a) return sign | 0x7fu;
+  if (a >= 448.0f) return sign | 0x7eu;
+  if (a < 0.015625f) return sign | static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
+  const int e = static_cast<int>((__float_as_uint(a) >> 23) & 0xffu) - 127;
+  const float unit = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);  // 2^-e, exact
+  int m = static_cast<int>(__builtin_rintf((a * unit - 1.0f) * 8.0f));
+  int exponent = e;
+  if (m == 8) {
+    m = 0;
+    exponent += 1;
+  }
+  uint32_t code = static_cast<uint32_t>(((exponent + 7) << 3) | m);
+  if (code > 0x7eu) code = 0x7eu;
+  return sign | code;
+}
+
+namespace {
+
+// ---- the activation quantiser -------------------------------------------------------------------------------
+
+constexpr int kQuantThreads = 256;
+
+struct QuantParams {
+  const void *input;
+  uint8_t *out;
+  float *scales;
+  const int32_t *row_limit;
+  int64_t rows;
+  int64_t width;
+  int32_t input_f32;
+};
+
+/// 16 lanes per 128-channel group, 8 channels each.
+__global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) {
+  const int64_t groups_per_row = p.width / 128;
+  const int64_t group = (static_cast<int64_t>(blockIdx.x) * kQuantThreads + threadIdx.x) / 16;
+  const int sub = static_cast<int>(threadIdx.x) & 15;
+  const int64_t row = group / groups_per_row;
+  const int64_t limit = p.row_limit != nullptr ? p.row_limit[0] : p.rows;
+  const bool active = row < p.rows && row < limit;
+  const int64_t column = (group % groups_per_row) * 128 + sub * 8;
+  float v[8];
+  if (active) {
+    if (p.input_f32) {
+      const float *src = static_cast<const float *>(p.input) + row * p.width + column;
+      const float4 lo = *reinterpret_cast<const float4 *>(src);
+      const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    } else {
+      const u32x4 packed = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p.input) + row * p.width + column);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(packed[j] << 16);
+        v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+#pragma unroll
+  for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+  if (!active) return;
+  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    lo |= e4m3_encode(v[j] / scale) << (8 * j);
+    hi |= e4m3_encode(v[j + 4] / scale) << (8 * j);
+  }
+  *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = make_uint2(lo, hi);
+  if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
+}
+
+// ---- grouped products --------------------------------------------------------------------------------------
+
+constexpr int kTileRows = 128;
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ intx8 load32(const uint8_t *pointer) {
+  const u32x4 lo = *reinterpret_cast<const u32x4 *>(pointer);
+  const u32x4 hi = *reinterpret_cast<const u32x4 *>(pointer + 16);
+  return intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+               static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+}
+
+__device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
+  uint2 packed;
+  packed.x = pack_bf16x2(v[0], v[1]);
+  packed.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2 *>(pointer) = packed;
+}
+
+constexpr int kPassTiles = 2;
+
+/// Decode-shaped: as the bf16 stream kernel, one 128-deep scale block per chunk.
+template <bool kGated>
+__global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p) {
+  const int tile = static_cast<int>(blockIdx.x);
+  if (tile >= p.num_tiles[0]) return;
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int64_t kb_count = p.K / 128;
+
+  int64_t n0, n1;
+  if constexpr (kGated) {
+    n0 = static_cast<int64_t>(blockIdx.y) * 64 + wave * 16;
+    n1 = p.out_width + n0;
+  } else {
+    n0 = static_cast<int64_t>(blockIdx.y) * 128 + wave * 32;
+    n1 = n0 + 16;
+    if (n0 >= p.out_width) return;
+  }
+  const uint8_t *w0 = p.weights + (expert * p.n_total + n0 + r16) * p.K + g * 32;
+  const uint8_t *w1 = p.weights + (expert * p.n_total + n1 + r16) * p.K + g * 32;
+  const float *ws0 = p.weight_scales + (expert * (p.n_total / 128) + n0 / 128) * kb_count;
+  const float *ws1 = p.weight_scales + (expert * (p.n_total / 128) + n1 / 128) * kb_count;
+
+  for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
+    const uint8_t *a[kPassTiles];
+    const float *as[kPassTiles];
+    bool valid[kPassTiles];
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      valid[ms] = m < rows;
+      int64_t source = first + m;
+      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      if (!valid[ms]) source = 0;
+      a[ms] = p.act + source * p.K + g * 32;
+      as[ms] = p.act_scales + source * kb_count;
+    }
+    floatx4 acc[2][kPassTiles];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    intx8 wcur[2], wnext[2], acur[kPassTiles], anext[kPassTiles];
+    float scur[2 + kPassTiles], snext[2 + kPassTiles];
+    auto fetch = [&](int64_t kb, intx8 (&w)[2], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
+      w[0] = load32(w0 + kb * 128);
+      w[1] = load32(w1 + kb * 128);
+      s[0] = ws0[kb];
+      s[1] = ws1[kb];
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms) {
+        x[ms] = valid[ms] ? load32(a[ms] + kb * 128) : intx8{0, 0, 0, 0, 0, 0, 0, 0};
+        s[2 + ms] = valid[ms] ? as[ms][kb] : 0.0f;
+      }
+    };
+    auto compute = [&](const intx8 (&w)[2], const intx8 (&x)[kPassTiles], const float (&s)[2 + kPassTiles]) {
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms)
+#pragma unroll
+        for (int set = 0; set < 2; ++set) {
+          const floatx4 block = mfma_16x16x128_fp8(w[set], x[ms], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+          const float scale = s[set] * s[2 + ms];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[set][ms][i] = __builtin_fmaf(block[i], scale, acc[set][ms][i]);
+        }
+    };
+    fetch(0, wcur, acur, scur);
+    for (int64_t kb = 0; kb < kb_count; kb += 2) {
+      if (kb + 1 < kb_count) fetch(kb + 1, wnext, anext, snext);
+      compute(wcur, acur, scur);
+      if (kb + 2 < kb_count) fetch(kb + 2, wcur, acur, scur);
+      if (kb + 1 < kb_count) compute(wnext, anext, snext);
+    }
+
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      if (m >= rows) continue;
+      uint16_t *row = p.out + (first + m) * p.out_width;
+      if constexpr (kGated) {
+        floatx4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        store_bf16x4(row + n0 + 4 * g, h);
+      } else {
+        store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
+        store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
+      }
+    }
+  }
+}
+
+/// Prefill-shaped: 128 x 128 tiles, one 128-deep scale block per LDS stage (16 KB per operand).
+constexpr int kStageChunks = 128 * 8;  // 16-byte chunks: 128 rows x 128 bytes
+
+__device__ __forceinline__ int swizzled(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+template <bool kGated>
+__global__ void __launch_bounds__(kThreads) tiled_fp8_kernel(GroupedFp8Params p) {
+  __shared__ u32x4 shared_a[2][kStageChunks];
+  __shared__ u32x4 shared_w[2][kStageChunks];
+  const int tile = static_cast<int>(blockIdx.x);
+  if (tile >= p.num_tiles[0]) return;
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int t = static_cast<int>(threadIdx.x);
+  const int wave = t / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int wm = wave & 1;
+  const int wn = wave >> 1;
+  const int64_t slice = static_cast<int64_t>(blockIdx.y) * (kGated ? 64 : 128);
+  const int64_t kb_count = p.K / 128;
+  const int64_t nb_count = p.n_total / 128;
+
+  const int chunk = t & 7;
+  const uint8_t *a_row[4];
+  const uint8_t *w_row[4];
+  bool a_valid[4], w_valid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (t >> 3) + 32 * i;
+    a_valid[i] = r < rows;
+    int64_t source = first + r;
+    if constexpr (kGated) source = a_valid[i] ? p.permuted_to_expanded[first + r] / p.top : 0;
+    a_row[i] = p.act + (a_valid[i] ? source : 0) * p.K + chunk * 16;
+    int64_t n;
+    if constexpr (kGated) n = r < 64 ? slice + r : p.out_width + slice + (r - 64);
+    else n = slice + r;
+    w_valid[i] = kGated ? true : n < p.out_width;
+    w_row[i] = p.weights + (expert * p.n_total + (w_valid[i] ? n : 0)) * p.K + chunk * 16;
+  }
+  // The activation scales of this lane's four MFMA rows, and the weight block of each row set.
+  const float *row_scale[4];
+  bool row_valid[4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const int m = wm * 64 + mi * 16 + r16;
+    row_valid[mi] = m < rows;
+    int64_t source = first + m;
+    if constexpr (kGated) source = row_valid[mi] ? p.permuted_to_expanded[first + m] / p.top : 0;
+    row_scale[mi] = p.act_scales + (row_valid[mi] ? source : 0) * kb_count;
+  }
+  const float *wscale_lo;  // FC1: the up rows; FC2: rows [slice, slice + 128)
+  const float *wscale_hi;  // FC1: the gate rows
+  if constexpr (kGated) {
+    wscale_lo = p.weight_scales + (expert * nb_count + slice / 128) * kb_count;
+    wscale_hi = p.weight_scales + (expert * nb_count + (p.out_width + slice) / 128) * kb_count;
+  } else {
+    wscale_lo = p.weight_scales + (expert * nb_count + slice / 128) * kb_count;
+    wscale_hi = wscale_lo;
+  }
+
+  u32x4 staged_a[4], staged_w[4];
+  auto fetch = [&](int64_t kb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      staged_a[i] = a_valid[i] ? *reinterpret_cast<const u32x4 *>(a_row[i] + kb * 128) : u32x4{0, 0, 0, 0};
+      staged_w[i] = w_valid[i] ? *reinterpret_cast<const u32x4 *>(w_row[i] + kb * 128) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto deposit = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (t >> 3) + 32 * i;
+      shared_a[stage][swizzled(r, chunk)] = staged_a[i];
+      shared_w[stage][swizzled(r, chunk)] = staged_w[i];
+    }
+  };
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) acc[ni][mi] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  fetch(0);
+  deposit(0);
+  __syncthreads();
+  for (int64_t kb = 0; kb < kb_count; ++kb) {
+    const int stage = static_cast<int>(kb & 1);
+    if (kb + 1 < kb_count) fetch(kb + 1);
+    float sx[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) sx[mi] = row_valid[mi] ? row_scale[mi][kb] : 0.0f;
+    const float sw_lo = wscale_lo[kb];
+    const float sw_hi = wscale_hi[kb];
+    // Lane group g takes 16-byte chunks 2g and 2g + 1 of the 128-byte row: 32 K elements.
+    intx8 wf[4], af[4];
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      int r;
+      if constexpr (kGated) r = (ni < 2 ? wn * 32 + ni * 16 : 64 + wn * 32 + (ni - 2) * 16) + r16;
+      else r = wn * 64 + ni * 16 + r16;
+      const u32x4 lo = shared_w[stage][swizzled(r, 2 * g)];
+      const u32x4 hi = shared_w[stage][swizzled(r, 2 * g + 1)];
+      wf[ni] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                     static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int r = wm * 64 + mi * 16 + r16;
+      const u32x4 lo = shared_a[stage][swizzled(r, 2 * g)];
+      const u32x4 hi = shared_a[stage][swizzled(r, 2 * g + 1)];
+      af[mi] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                     static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+    }
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const float sw = (kGated ? ni < 2 : true) ? sw_lo : sw_hi;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const floatx4 block = mfma_16x16x128_fp8(wf[ni], af[mi], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+        const float scale = sw * sx[mi];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ni][mi][i] = __builtin_fmaf(block[i], scale, acc[ni][mi][i]);
+      }
+    }
+    if (kb + 1 < kb_count) deposit(stage ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const int m = wm * 64 + mi * 16 + r16;
+    if (m >= rows) continue;
+    uint16_t *row = p.out + (first + m) * p.out_width;
+    if constexpr (kGated) {
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        floatx4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = silu(acc[ni + 2][mi][i]) * acc[ni][mi][i];
+        store_bf16x4(row + slice + wn * 32 + ni * 16 + 4 * g, h);
+      }
+    } else {
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        const int64_t col = slice + wn * 64 + ni * 16 + 4 * g;
+        if (col < p.out_width) store_bf16x4(row + col, acc[ni][mi]);
+      }
+    }
+  }
+}
+
+constexpr int64_t kStreamRowsPerExpert = 24;
+
+}  // namespace
+
+void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
+                         const int32_t *row_limit, int64_t rows, int64_t width, hipStream_t stream) {
+  QuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0};
+  const int64_t groups = rows * (width / 128);
+  const int64_t blocks = ceil_div<int64_t>(groups * 16, kQuantThreads);
+  hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQuantThreads), 0, stream, p);
+}
+
+void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
+                        hipStream_t stream) {
+  const int64_t slices = gated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
+  const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices));
+  if (stream_path) {
+    if (gated) hipLaunchKernelGGL(stream_fp8_kernel<true>, grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(stream_fp8_kernel<false>, grid, dim3(kThreads), 0, stream, p);
+  } else {
+    if (gated) hipLaunchKernelGGL(tiled_fp8_kernel<true>, grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(tiled_fp8_kernel<false>, grid, dim3(kThreads), 0, stream, p);
+  }
+}
+
+bool fp8_stream_path(int64_t routes, int64_t experts) { return routes < kStreamRowsPerExpert * experts; }
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_quantize_fp8(const uniserve_quantize_fp8_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->input == nullptr || call->out == nullptr || call->scales == nullptr)
+      return UNISERVE_REFUSE(call, "quantize_fp8 needs input, out and scales");
+    if (call->group != 128) return UNISERVE_REFUSE(call, "quantize_fp8 quantises groups of 128 channels");
+    if (call->width <= 0 || call->width % 128 != 0)
+      return UNISERVE_REFUSE(call, "quantize_fp8 needs a width of whole 128-channel groups");
+    if (call->input_dtype != UNISERVE_DTYPE_BF16 && call->input_dtype != UNISERVE_DTYPE_F32)
+      return UNISERVE_REFUSE(call, "quantize_fp8 reads bf16 or f32 rows");
+    if (call->rows < 0) return UNISERVE_REFUSE(call, "quantize_fp8 needs a non-negative row count");
+    if (call->rows == 0) return 0;
+    launch_quantize_fp8(call->input, call->input_dtype == UNISERVE_DTYPE_F32, static_cast<uint8_t *>(call->out),
+                        call->scales, call->row_limit, call->rows, call->width, static_cast<hipStream_t>(stream));
+    return launched(call, "quantize_fp8");
+  });
+}
+
+extern "C" int32_t uniserve_gather_gemm_fp8(const uniserve_gather_fp8_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_fp8 writes bf16 only");
+    if (call->block_n != 128 || call->block_k != 128)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 serves 128 x 128 weight blocks");
+    if (call->hidden == nullptr || call->hidden_scales == nullptr || call->weights == nullptr ||
+        call->weight_scales == nullptr || call->out == nullptr)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs hidden, weights, their scales and out");
+    if (call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->permuted_to_expanded == nullptr || call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs the sort's tile and route maps");
+    if (call->multiprocessors <= 0) return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs its device's multiprocessor count");
+    if (call->hidden_size <= 0 || call->hidden_size % 128 != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs a hidden size of whole 128-element blocks");
+    if (call->width <= 0 || call->width % 256 != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs an intermediate width of whole 128-row blocks");
+    if (call->tokens < 0 || call->top <= 0 || call->experts <= 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs non-negative tokens and positive top and experts");
+    if (call->permuted_rows < call->tokens * call->top || call->permuted_rows % kTileRows != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs whole 128-row tiles that hold every route");
+    const int64_t max_tiles = call->permuted_rows / kTileRows;
+    if (max_tiles == 0) return 0;
+    GroupedFp8Params p{};
+    p.act = static_cast<const uint8_t *>(call->hidden);
+    p.act_scales = call->hidden_scales;
+    p.weights = static_cast<const uint8_t *>(call->weights);
+    p.weight_scales = call->weight_scales;
+    p.out = static_cast<uint16_t *>(call->out);
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.num_tiles = call->num_non_exiting_tiles;
+    p.K = call->hidden_size;
+    p.n_total = call->width;
+    p.out_width = call->width / 2;
+    p.top = call->top;
+    launch_grouped_fp8(p, true, max_tiles, fp8_stream_path(call->tokens * call->top, call->experts),
+                       static_cast<hipStream_t>(stream));
+    return launched(call, "gather_gemm_fp8");
+  });
+}
+
+extern "C" int32_t uniserve_route_gemm_fp8(const uniserve_route_fp8_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "route_gemm_fp8 writes bf16 only");
+    if (call->block_n != 128 || call->block_k != 128)
+      return UNISERVE_REFUSE(call, "route_gemm_fp8 serves 128 x 128 weight blocks");
+    if (call->rows == nullptr || call->row_scales == nullptr || call->weights == nullptr ||
+        call->weight_scales == nullptr || call->out == nullptr)
+      return UNISERVE_REFUSE(call, "route_gemm_fp8 needs rows, weights, their scales and out");
+    if (call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->permuted_to_expanded == nullptr || call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "route_gemm_fp8 needs the sort's tile and route maps");
+    if (call->multiprocessors <= 0) return UNISERVE_REFUSE(call, "route_gemm_fp8 needs its device's multiprocessor count");
+    if (call->intermediate <= 0 || call->intermediate % 128 != 0)
+      return UNISERVE_REFUSE(call, "route_gemm_fp8 needs an intermediate width of whole 128-element blocks");
+    if (call->width <= 0 || call->width % 128 != 0)
+      return UNISERVE_REFUSE(call, "route_gemm_fp8 needs a hidden width of whole 128-row blocks");
+    if (call->experts <= 0) return UNISERVE_REFUSE(call, "route_gemm_fp8 needs positive experts");
+    if (call->permuted_rows < 0 || call->permuted_rows % kTileRows != 0)
+      return UNISERVE_REFUSE(call, "route_gemm_fp8 needs permuted rows of whole 128-row tiles");
+    const int64_t max_tiles = call->permuted_rows / kTileRows;
+    if (max_tiles == 0) return 0;
+    GroupedFp8Params p{};
+    p.act = static_cast<const uint8_t *>(call->rows);
+    p.act_scales = call->row_scales;
+    p.weights = static_cast<const uint8_t *>(call->weights);
+    p.weight_scales = call->weight_scales;
+    p.out = static_cast<uint16_t *>(call->out);
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.num_tiles = call->num_non_exiting_tiles;
+    p.K = call->intermediate;
+    p.n_total = call->width;
+    p.out_width = call->width;
+    p.top = 1;
+    const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
+    launch_grouped_fp8(p, false, max_tiles, fp8_stream_path(routes_bound, call->experts),
+                       static_cast<hipStream_t>(stream));
+    return launched(call, "route_gemm_fp8");
+  });
+}

@@ -1,0 +1,281 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The routed MoE layer as one call: `MoE::routed` (crates/nn/src/modules/moe.rs:770-795) issues
+// router gemm -> topk_softmax -> moe_sort -> gather_gemm -> route_gemm -> moe_unpermute, in that
+// order (the order crates/nn/tests/moe.rs:1402-1438 records); this driver issues the same entries
+// on one stream over intermediates carved from a caller-owned workspace, so it allocates nothing,
+// reads nothing back and can be captured into a HIP graph. With e4m3 weights the activations of
+// each product are quantised per row per 128 channels first (two more launches).
+#include <cstring>
+
+#include "common.hpp"
+#include "grouped_fp8.hpp"
+#include "router_gemm.hpp"
+#include "uniserve_gather_gemm.h"
+#include "uniserve_moe_fp8.h"
+#include "uniserve_moe_layer.h"
+#include "uniserve_moe_sort.h"
+#include "uniserve_moe_unpermute.h"
+#include "uniserve_route_gemm.h"
+#include "uniserve_topk_softmax.h"
+
+namespace {
+
+constexpr int64_t kTile = 128;
+constexpr int64_t kAlign = 256;
+
+int64_t aligned(int64_t bytes) { return (bytes + kAlign - 1) / kAlign * kAlign; }
+
+bool views_of(int64_t tokens, int64_t hidden, int64_t experts, int64_t top, int64_t intermediate,
+              int64_t weight_dtype, uniserve_moe_layer_views *v) {
+  if (tokens < 0 || hidden <= 0 || experts <= 0 || top <= 0 || top > experts || intermediate <= 0) return false;
+  if (weight_dtype != UNISERVE_DTYPE_BF16 && weight_dtype != UNISERVE_DTYPE_F8E4M3) return false;
+  std::memset(v, 0, sizeof(*v));
+  v->max_tiles = uniserve_moe_max_tiles(tokens, top, experts, kTile);
+  v->permuted_rows = v->max_tiles * kTile;
+  int64_t at = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t here = at;
+    at += aligned(bytes > 0 ? bytes : 1);
+    return here;
+  };
+  v->scores = take(tokens * experts * 2);
+  v->ids = take(tokens * top * 4);
+  v->weights = take(tokens * top * 4);
+  v->tile_to_expert = take(v->max_tiles * 4);
+  v->tile_to_limit = take(v->max_tiles * 4);
+  v->expanded_to_permuted = take(tokens * top * 4);
+  v->permuted_to_expanded = take(v->permuted_rows * 4);
+  v->permuted_to_token = take(v->permuted_rows * 4);
+  v->total_padded_tokens = take(4);
+  v->num_non_exiting_tiles = take(4);
+  v->gated = take(v->permuted_rows * intermediate * 2);
+  v->products = take(v->permuted_rows * hidden * 2);
+  if (weight_dtype == UNISERVE_DTYPE_F8E4M3) {
+    v->hidden_q = take(tokens * hidden);
+    v->hidden_s = take(tokens * (hidden / 128) * 4);
+    v->gated_q = take(v->permuted_rows * intermediate);
+    v->gated_s = take(v->permuted_rows * (intermediate / 128) * 4);
+  } else {
+    v->hidden_q = v->hidden_s = v->gated_q = v->gated_s = -1;
+  }
+  v->total = at;
+  return true;
+}
+
+template <class Call>
+int32_t forward_error(const uniserve_moe_layer_call *layer, const char *stage, const Call &inner) {
+  return ::uniserve::refuse_into(const_cast<char *>(layer->error), "%s: %s", stage, inner.error);
+}
+
+}  // namespace
+
+extern "C" int64_t uniserve_moe_max_tiles(int64_t tokens, int64_t top, int64_t local_experts, int64_t tile) {
+  const int64_t expanded = tokens * top;
+  if (expanded <= local_experts || tile == 0) return expanded;
+  return (expanded + (tile - 1) * local_experts) / tile;
+}
+
+extern "C" int32_t uniserve_moe_layer_views_of(int64_t tokens, int64_t hidden_size, int64_t experts,
+                                               int64_t top, int64_t intermediate, int64_t weight_dtype,
+                                               uniserve_moe_layer_views *views) {
+  if (views == nullptr) return 1;
+  return views_of(tokens, hidden_size, experts, top, intermediate, weight_dtype, views) ? 0 : 1;
+}
+
+extern "C" int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_size, int64_t experts,
+                                                int64_t top, int64_t intermediate, int64_t weight_dtype) {
+  uniserve_moe_layer_views v;
+  if (!views_of(tokens, hidden_size, experts, top, intermediate, weight_dtype, &v)) return -1;
+  return v.total;
+}
+
+extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->hidden == nullptr || call->router == nullptr || call->up_gate == nullptr ||
+        call->down == nullptr || call->out == nullptr || call->workspace == nullptr)
+      return UNISERVE_REFUSE(call, "moe_layer needs hidden, router, both stacks, out and a workspace");
+    const bool fp8 = call->weight_dtype == UNISERVE_DTYPE_F8E4M3;
+    if (fp8 && (call->up_gate_scales == nullptr || call->down_scales == nullptr))
+      return UNISERVE_REFUSE(call, "moe_layer: e4m3 stacks need their block scales");
+    if (reinterpret_cast<uintptr_t>(call->workspace) % kAlign != 0)
+      return UNISERVE_REFUSE(call, "moe_layer needs a 256-byte aligned workspace");
+    uniserve_moe_layer_views v;
+    if (!views_of(call->tokens, call->hidden_size, call->experts, call->top, call->intermediate,
+                  call->weight_dtype, &v))
+      return UNISERVE_REFUSE(call, "moe_layer does not serve these extents or this weight type");
+    if (call->workspace_bytes < v.total)
+      return UNISERVE_REFUSE(call, "moe_layer needs %lld workspace bytes, has %lld",
+                             static_cast<long long>(v.total), static_cast<long long>(call->workspace_bytes));
+    if (call->tokens == 0) return 0;
+    if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
+
+    char *ws = static_cast<char *>(call->workspace);
+    auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t *ids = static_cast<int32_t *>(at(v.ids));
+    float *weights = static_cast<float *>(at(v.weights));
+    int32_t *t2e = static_cast<int32_t *>(at(v.tile_to_expert));
+    int32_t *t2l = static_cast<int32_t *>(at(v.tile_to_limit));
+    int32_t *e2p = static_cast<int32_t *>(at(v.expanded_to_permuted));
+    int32_t *p2e = static_cast<int32_t *>(at(v.permuted_to_expanded));
+    int32_t *p2t = static_cast<int32_t *>(at(v.permuted_to_token));
+    int32_t *padded = static_cast<int32_t *>(at(v.total_padded_tokens));
+    int32_t *tiles = static_cast<int32_t *>(at(v.num_non_exiting_tiles));
+
+    // 1. Router scores, bf16 (the router Linear's output dtype).
+    RouterParams rp{static_cast<const uint16_t *>(call->hidden), static_cast<const uint16_t *>(call->router),
+                    static_cast<uint16_t *>(at(v.scores)), call->router_bias, call->tokens, call->experts,
+                    call->hidden_size, call->hidden_size, call->hidden_size, call->experts, 1.0f};
+    launch_router(rp, s);
+    if (int32_t status = launched(call, "router gemm")) return status;
+
+    // 2. topk_softmax over the bf16 scores.
+    char message[512] = {0};
+    if (uniserve_topk_softmax_launch(at(v.scores), 1, call->experts, static_cast<int32_t>(call->tokens),
+                                     static_cast<int32_t>(call->experts), static_cast<int32_t>(call->top),
+                                     call->renormalize ? 1 : 0, nullptr, -1, ids, weights, nullptr,
+                                     reinterpret_cast<const uint32_t *>(call->live_tokens), nullptr, stream,
+                                     message, sizeof(message)) != 0)
+      return UNISERVE_REFUSE(call, "topk_softmax: %s", message);
+
+    // 3. moe_sort over every expert.
+    uniserve_moe_sort_call sort{};
+    sort.ids = ids;
+    sort.scales = weights;
+    sort.tile_to_expert = t2e;
+    sort.tile_to_limit = t2l;
+    sort.expanded_to_permuted = e2p;
+    sort.permuted_to_expanded = p2e;
+    sort.total_padded_tokens = padded;
+    sort.num_non_exiting_tiles = tiles;
+    sort.tokens = call->tokens;
+    sort.top = call->top;
+    sort.experts = call->experts;
+    sort.local_experts = call->experts;
+    sort.local_offset = 0;
+    sort.tile_tokens = kTile;
+    sort.scales_dtype = UNISERVE_DTYPE_F32;
+    sort.live_tokens = call->live_tokens;
+    sort.permuted_to_token = p2t;
+    if (uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
+
+    // 4-5. The two products.
+    if (!fp8) {
+      uniserve_gather_call fc1{};
+      fc1.hidden = call->hidden;
+      fc1.weights = call->up_gate;
+      fc1.out = at(v.gated);
+      fc1.tile_to_expert = t2e;
+      fc1.tile_to_limit = t2l;
+      fc1.permuted_to_expanded = p2e;
+      fc1.num_non_exiting_tiles = tiles;
+      fc1.tokens = call->tokens;
+      fc1.permuted_rows = v.permuted_rows;
+      fc1.width = 2 * call->intermediate;
+      fc1.hidden_size = call->hidden_size;
+      fc1.experts = call->experts;
+      fc1.top = call->top;
+      fc1.dtype = UNISERVE_DTYPE_BF16;
+      fc1.multiprocessors = call->multiprocessors;
+      if (uniserve_gather_gemm(&fc1, stream) != 0) return forward_error(call, "gather_gemm", fc1);
+
+      uniserve_route_call fc2{};
+      fc2.rows = at(v.gated);
+      fc2.weights = call->down;
+      fc2.out = at(v.products);
+      fc2.tile_to_expert = t2e;
+      fc2.tile_to_limit = t2l;
+      fc2.permuted_to_expanded = p2e;
+      fc2.num_non_exiting_tiles = tiles;
+      fc2.permuted_rows = v.permuted_rows;
+      fc2.width = call->hidden_size;
+      fc2.intermediate = call->intermediate;
+      fc2.experts = call->experts;
+      fc2.dtype = UNISERVE_DTYPE_BF16;
+      fc2.multiprocessors = call->multiprocessors;
+      if (uniserve_route_gemm(&fc2, stream) != 0) return forward_error(call, "route_gemm", fc2);
+    } else {
+      uniserve_quantize_fp8_call qx{};
+      qx.input = call->hidden;
+      qx.out = at(v.hidden_q);
+      qx.scales = static_cast<float *>(at(v.hidden_s));
+      qx.rows = call->tokens;
+      qx.width = call->hidden_size;
+      qx.input_dtype = UNISERVE_DTYPE_BF16;
+      qx.group = 128;
+      if (uniserve_quantize_fp8(&qx, stream) != 0) return forward_error(call, "quantize_fp8", qx);
+
+      uniserve_gather_fp8_call fc1{};
+      fc1.hidden = at(v.hidden_q);
+      fc1.hidden_scales = static_cast<const float *>(at(v.hidden_s));
+      fc1.weights = call->up_gate;
+      fc1.weight_scales = call->up_gate_scales;
+      fc1.out = at(v.gated);
+      fc1.tile_to_expert = t2e;
+      fc1.tile_to_limit = t2l;
+      fc1.permuted_to_expanded = p2e;
+      fc1.num_non_exiting_tiles = tiles;
+      fc1.tokens = call->tokens;
+      fc1.permuted_rows = v.permuted_rows;
+      fc1.width = 2 * call->intermediate;
+      fc1.hidden_size = call->hidden_size;
+      fc1.experts = call->experts;
+      fc1.top = call->top;
+      fc1.block_n = 128;
+      fc1.block_k = 128;
+      fc1.out_dtype = UNISERVE_DTYPE_BF16;
+      fc1.multiprocessors = call->multiprocessors;
+      if (uniserve_gather_gemm_fp8(&fc1, stream) != 0) return forward_error(call, "gather_gemm_fp8", fc1);
+
+      uniserve_quantize_fp8_call qg{};
+      qg.input = at(v.gated);
+      qg.out = at(v.gated_q);
+      qg.scales = static_cast<float *>(at(v.gated_s));
+      qg.row_limit = padded;
+      qg.rows = v.permuted_rows;
+      qg.width = call->intermediate;
+      qg.input_dtype = UNISERVE_DTYPE_BF16;
+      qg.group = 128;
+      if (uniserve_quantize_fp8(&qg, stream) != 0) return forward_error(call, "quantize_fp8", qg);
+
+      uniserve_route_fp8_call fc2{};
+      fc2.rows = at(v.gated_q);
+      fc2.row_scales = static_cast<const float *>(at(v.gated_s));
+      fc2.weights = call->down;
+      fc2.weight_scales = call->down_scales;
+      fc2.out = at(v.products);
+      fc2.tile_to_expert = t2e;
+      fc2.tile_to_limit = t2l;
+      fc2.permuted_to_expanded = p2e;
+      fc2.num_non_exiting_tiles = tiles;
+      fc2.permuted_rows = v.permuted_rows;
+      fc2.width = call->hidden_size;
+      fc2.intermediate = call->intermediate;
+      fc2.experts = call->experts;
+      fc2.block_n = 128;
+      fc2.block_k = 128;
+      fc2.out_dtype = UNISERVE_DTYPE_BF16;
+      fc2.multiprocessors = call->multiprocessors;
+      if (uniserve_route_gemm_fp8(&fc2, stream) != 0) return forward_error(call, "route_gemm_fp8", fc2);
+    }
+
+    // 6. The weighted combine, permuted layout.
+    uniserve_unpermute_call combine{};
+    combine.routes = at(v.products);
+    combine.out = call->out;
+    combine.expanded_to_permuted = e2p;
+    combine.scales = weights;
+    combine.tokens = call->tokens;
+    combine.top = call->top;
+    combine.hidden = call->hidden_size;
+    combine.routes_rows = v.permuted_rows;
+    combine.input_dtype = UNISERVE_DTYPE_BF16;
+    combine.scales_dtype = UNISERVE_DTYPE_F32;
+    combine.output_dtype = UNISERVE_DTYPE_BF16;
+    combine.layout = UNISERVE_UNPERMUTE_LAYOUT_PERMUTED;
+    if (uniserve_moe_unpermute(&combine, stream) != 0) return forward_error(call, "moe_unpermute", combine);
+    return 0;
+  });
+}

@@ -1,0 +1,230 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// moe_sort on gfx950 (operator: crates/ops/src/moe/sort.rs; reference package:
+// crates/ops/kernels/moe_sort/trtllm). Groups the held routes of a `tokens x top` routing by local
+// expert, each expert's routes in ascending expanded-route order from a tile boundary, and writes
+// the tile tables, the three maps and the two counts. Integer work, exact.
+//
+// One launch, no scratch memory. Workgroup b owns the chunk [b * kChunk, (b + 1) * kChunk) of the
+// routes and computes everything it needs itself:
+//
+//   1. count every held route by expert (the totals) and those before its chunk (its base within
+//      each expert), reading the whole `ids` vector - a few hundred KB from L2 even at 8192 tokens
+//      x 8, cheaper than a second launch and a global barrier;
+//   2. the tiles per expert and their exclusive scan (workgroup 0 also writes the tile tables, the
+//      padding rows and the counts);
+//   3. place its chunk: each wavefront owns a contiguous slice, counts it per expert, a scan over
+//      the wavefronts turns the counts into starting rows, and the slice is walked again in order.
+//
+// Routes naming the same expert within one wavefront are found with a ballot per key bit (the
+// wave64 form of a match-any), so each (wave, expert) group costs one LDS update and the rank of a
+// route within its group is a popcount of the lanes below it - which keeps the order stable.
+#include "common.hpp"
+#include "uniserve_moe_sort.h"
+
+namespace uniserve {
+namespace {
+
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / kWave;
+constexpr int64_t kChunk = 4096;
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+
+struct SortParams {
+  const int32_t *ids;
+  int32_t *tile_to_expert;
+  int32_t *tile_to_limit;
+  int32_t *expanded_to_permuted;
+  int32_t *permuted_to_expanded;
+  int32_t *permuted_to_token;
+  int32_t *total_padded_tokens;
+  int32_t *num_non_exiting_tiles;
+  const int32_t *live_tokens;
+  int64_t routes;
+  int64_t top;
+  int32_t local_experts;
+  int32_t local_offset;
+  int32_t tile;
+  int32_t key_bits;  ///< bits of (local expert + 1), the match key
+};
+
+/// The local expert of route `route`, or -1 when it is not live or not in the window.
+__device__ __forceinline__ int32_t local_expert(const SortParams &p, int64_t route, int64_t live) {
+  if (route >= p.routes || route >= live) return -1;
+  const int64_t local = static_cast<int64_t>(p.ids[route]) - p.local_offset;
+  return (local >= 0 && local < p.local_experts) ? static_cast<int32_t>(local) : -1;
+}
+
+__global__ void __launch_bounds__(kSortThreads) moe_sort_kernel(SortParams p) {
+  extern __shared__ int32_t lds[];
+  const int E = p.local_experts;
+  int32_t *total = lds;                  // [E] held routes per expert
+  int32_t *before = total + E;           // [E] held routes per expert before this chunk
+  int32_t *first_row = before + E;       // [E] first permuted row of each expert
+  int32_t *wave_rows = first_row + E;    // [kSortWaves][E] per-wave counts, then start rows
+
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
+  const int64_t chunk_first = static_cast<int64_t>(blockIdx.x) * kChunk;
+  const int64_t chunk_past = chunk_first + kChunk < p.routes ? chunk_first + kChunk : p.routes;
+
+  for (int i = threadIdx.x; i < (3 + kSortWaves) * E; i += kSortThreads) lds[i] = 0;
+  __syncthreads();
+
+  // 1. Totals and this chunk's bases. kChunk is a multiple of the wavefront, so a group of 64
+  //    routes lies wholly before the chunk or not.
+  for (int64_t base = static_cast<int64_t>(wave) * kWave; base < p.routes; base += kSortThreads) {
+    const int32_t e = local_expert(p, base + lane, live);
+    const uint64_t peers = match_any(static_cast<uint32_t>(e + 1), p.key_bits);
+    if (e >= 0 && (peers & below) == 0) {
+      const int n = __popcll(peers);
+      atomicAdd(&total[e], n);
+      if (base < chunk_first) atomicAdd(&before[e], n);
+    }
+  }
+  __syncthreads();
+
+  // 2. Each expert's first tile: an exclusive scan of the tile counts by the first wavefront,
+  //    64 experts at a time.
+  if (wave == 0) {
+    int32_t carried = 0;
+    for (int first = 0; first < E; first += kWave) {
+      const int e = first + lane;
+      const int32_t tiles = e < E ? (total[e] + p.tile - 1) / p.tile : 0;
+      int32_t inclusive = tiles;
+#pragma unroll
+      for (int offset = 1; offset < kWave; offset *= 2) {
+        const int32_t other = __shfl_up(inclusive, offset);
+        if (lane >= offset) inclusive += other;
+      }
+      if (e < E) first_row[e] = (carried + inclusive - tiles) * p.tile;
+      carried += __shfl(inclusive, kWave - 1);
+    }
+    if (blockIdx.x == 0 && lane == 0) {
+      p.total_padded_tokens[0] = carried * p.tile;
+      p.num_non_exiting_tiles[0] = carried;
+    }
+  }
+  __syncthreads();
+
+  if (blockIdx.x == 0) {
+    // The tile tables and the padding rows of each expert's last tile, one wavefront per expert.
+    for (int e = wave; e < E; e += kSortWaves) {
+      const int32_t count = total[e];
+      if (count == 0) continue;
+      const int32_t first = first_row[e];
+      const int32_t tiles = (count + p.tile - 1) / p.tile;
+      const int32_t first_tile = first / p.tile;
+      for (int32_t t = lane; t < tiles; t += kWave) {
+        const int32_t end_of_tile = (first_tile + t + 1) * p.tile;
+        const int32_t end_of_rows = first + count;
+        p.tile_to_expert[first_tile + t] = e;
+        p.tile_to_limit[first_tile + t] = end_of_tile < end_of_rows ? end_of_tile : end_of_rows;
+      }
+      for (int32_t row = count + lane; row < tiles * p.tile; row += kWave) {
+        p.permuted_to_expanded[first + row] = -1;
+        p.permuted_to_token[first + row] = -1;
+      }
+    }
+  }
+
+  // 3. Place this chunk. Wavefront w owns whole groups of 64 routes, a contiguous slice.
+  const int64_t groups = (chunk_past - chunk_first + kWave - 1) / kWave;
+  const int64_t own = (groups + kSortWaves - 1) / kSortWaves;
+  const int64_t slice_first = chunk_first + static_cast<int64_t>(wave) * own * kWave;
+  int64_t slice_past = slice_first + own * kWave;
+  if (slice_past > chunk_past) slice_past = chunk_past;
+  int32_t *mine = wave_rows + wave * E;
+
+  for (int64_t base = slice_first; base < slice_past; base += kWave) {
+    const int64_t route = base + lane;
+    const int32_t e = route < slice_past ? local_expert(p, route, live) : -1;
+    const uint64_t peers = match_any(static_cast<uint32_t>(e + 1), p.key_bits);
+    if (e >= 0 && (peers & below) == 0) mine[e] += __popcll(peers);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kSortThreads) {
+    int32_t running = first_row[e] + before[e];
+    for (int w = 0; w < kSortWaves; ++w) {
+      const int32_t count = wave_rows[w * E + e];
+      wave_rows[w * E + e] = running;
+      running += count;
+    }
+  }
+  __syncthreads();
+
+  for (int64_t base = slice_first; base < slice_past; base += kWave) {
+    const int64_t route = base + lane;
+    const bool inside = route < slice_past;
+    const int32_t e = inside ? local_expert(p, route, live) : -1;
+    const uint64_t peers = match_any(static_cast<uint32_t>(e + 1), p.key_bits);
+    if (e >= 0) {
+      const int32_t row = mine[e] + __popcll(peers & below);
+      p.expanded_to_permuted[route] = row;
+      p.permuted_to_expanded[row] = static_cast<int32_t>(route);
+      p.permuted_to_token[row] = static_cast<int32_t>(route / p.top);
+    } else if (inside) {
+      // -1: a live route of an expert this rank does not hold; -2: a route of a row the batch
+      // does not fill (crates/ops/src/moe/sort.rs:15-24).
+      p.expanded_to_permuted[route] = route < live ? -1 : -2;
+    }
+    // Every lane has read its group's start row before the group's first lane advances it.
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0 && (peers & below) == 0) mine[e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+}  // namespace
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_moe_sort(const uniserve_moe_sort_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    // The refusals of the reference entry (crates/ops/kernels/moe_sort/trtllm/src/entry.cpp:26-70).
+    if (call->ids == nullptr || call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->expanded_to_permuted == nullptr || call->permuted_to_expanded == nullptr ||
+        call->permuted_to_token == nullptr || call->total_padded_tokens == nullptr ||
+        call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "moe_sort needs the router's ids and all seven metadata buffers");
+    if (call->scales_dtype != UNISERVE_DTYPE_F32 && call->scales_dtype != UNISERVE_DTYPE_BF16 &&
+        call->scales_dtype != UNISERVE_DTYPE_F16)
+      return UNISERVE_REFUSE(call, "moe_sort serves f32, bf16 or fp16 route weights");
+    if (call->tokens < 0 || call->top < 0 || call->experts <= 0 || call->local_experts <= 0 ||
+        call->tile_tokens <= 0)
+      return UNISERVE_REFUSE(call, "moe_sort needs a non-negative route count and positive experts, local experts and tile");
+    if (call->local_offset < 0 || call->local_offset + call->local_experts > call->experts)
+      return UNISERVE_REFUSE(call, "moe_sort's local expert window lies outside the router's experts");
+    if (call->tokens * call->top > 0x7fffffffLL)
+      return UNISERVE_REFUSE(call, "moe_sort's expanded routes do not fit the metadata's int32 indexes");
+    const int64_t lds_bytes = (3 + kSortWaves) * call->local_experts * static_cast<int64_t>(sizeof(int32_t));
+    if (lds_bytes > kMaxLdsBytes)
+      return UNISERVE_REFUSE(call, "moe_sort's expert count outgrows one workgroup's LDS (%lld local experts)",
+                             static_cast<long long>(call->local_experts));
+
+    SortParams p{};
+    p.ids = call->ids;
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.expanded_to_permuted = call->expanded_to_permuted;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.permuted_to_token = call->permuted_to_token;
+    p.total_padded_tokens = call->total_padded_tokens;
+    p.num_non_exiting_tiles = call->num_non_exiting_tiles;
+    p.live_tokens = call->live_tokens;
+    p.routes = call->tokens * call->top;
+    p.top = call->top;
+    p.local_experts = static_cast<int32_t>(call->local_experts);
+    p.local_offset = static_cast<int32_t>(call->local_offset);
+    p.tile = static_cast<int32_t>(call->tile_tokens);
+    int bits = 0;
+    while ((1ll << bits) <= call->local_experts) ++bits;
+    p.key_bits = bits;
+    const int64_t chunks = p.routes == 0 ? 1 : ceil_div<int64_t>(p.routes, kChunk);
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(static_cast<uint32_t>(chunks)), dim3(kSortThreads),
+                       static_cast<size_t>(lds_bytes), static_cast<hipStream_t>(stream), p);
+    return launched(call, "moe_sort");
+  });
+}

@@ -1,0 +1,125 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// moe_unpermute on gfx950 (operator: crates/ops/src/moe/combine.rs; reference entry:
+// crates/ops/kernels/moe_unpermute/trtllm/src/entry.cpp):
+//
+//   out[t] = sum_{k visible} scales[t, k] * routes[row(t, k)]
+//
+// accumulated in FP32 in route order and rounded once into the output type. A route whose map entry
+// is negative (or names no row of `routes`) contributes nothing, so a token with no visible route is
+// exactly zero. HBM-bound: each lane moves 16 bytes (8 elements) of every route row of its token.
+#include "common.hpp"
+#include "uniserve_moe_unpermute.h"
+
+namespace uniserve {
+namespace {
+
+constexpr int kCombineThreads = 128;
+constexpr int kPerLane = 8;
+constexpr int kColumnsPerBlock = kCombineThreads * kPerLane;
+
+struct CombineParams {
+  const void *routes;
+  void *out;
+  const int32_t *expanded_to_permuted;
+  const void *scales;
+  int64_t top;
+  int64_t hidden;
+  int64_t routes_rows;
+  int32_t expanded;
+};
+
+template <class Element>
+__device__ __forceinline__ float widen(Element value);
+template <>
+__device__ __forceinline__ float widen<uint16_t>(uint16_t value) { return bf16_to_f32(value); }
+template <>
+__device__ __forceinline__ float widen<_Float16>(_Float16 value) { return static_cast<float>(value); }
+template <>
+__device__ __forceinline__ float widen<float>(float value) { return value; }
+
+template <class Element>
+__device__ __forceinline__ Element narrow(float value);
+template <>
+__device__ __forceinline__ uint16_t narrow<uint16_t>(float value) { return f32_to_bf16(value); }
+template <>
+__device__ __forceinline__ _Float16 narrow<_Float16>(float value) { return static_cast<_Float16>(value); }
+
+/// `Element` is the route/output type (uint16_t = bf16, _Float16 = f16), `Scale` the weights'.
+template <class Element, class Scale>
+__global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams p) {
+  const int64_t token = blockIdx.x;
+  const int64_t column = static_cast<int64_t>(blockIdx.y) * kColumnsPerBlock + threadIdx.x * kPerLane;
+  if (column >= p.hidden) return;
+  const Element *routes = static_cast<const Element *>(p.routes);
+  const Scale *scales = static_cast<const Scale *>(p.scales);
+  float sum[kPerLane];
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) sum[j] = 0.0f;
+  for (int64_t k = 0; k < p.top; ++k) {
+    const int64_t slot = token * p.top + k;
+    const int32_t entry = p.expanded_to_permuted[slot];
+    if (entry < 0 || entry >= p.routes_rows) continue;
+    const int64_t row = p.expanded ? slot : entry;
+    const float weight = widen<Scale>(scales[slot]);
+    const uint4 packed = *reinterpret_cast<const uint4 *>(routes + row * p.hidden + column);
+    const Element *values = reinterpret_cast<const Element *>(&packed);
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) sum[j] = __builtin_fmaf(weight, widen<Element>(values[j]), sum[j]);
+  }
+  Element result[kPerLane];
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) result[j] = narrow<Element>(sum[j]);
+  *reinterpret_cast<uint4 *>(static_cast<Element *>(p.out) + token * p.hidden + column) =
+      *reinterpret_cast<const uint4 *>(result);
+}
+
+}  // namespace
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_moe_unpermute(const uniserve_unpermute_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->input_dtype != call->output_dtype)
+      return UNISERVE_REFUSE(call, "moe_unpermute needs one input and output dtype");
+    if (call->routes == nullptr || call->out == nullptr || call->expanded_to_permuted == nullptr ||
+        call->scales == nullptr)
+      return UNISERVE_REFUSE(call, "moe_unpermute needs routes, out, expanded_to_permuted and scales");
+    if (call->hidden % 8 != 0 || call->hidden <= 0)
+      return UNISERVE_REFUSE(call, "moe_unpermute needs a hidden width of whole 8-element groups");
+    if (call->tokens < 0 || call->top <= 0 || call->routes_rows < 0)
+      return UNISERVE_REFUSE(call, "moe_unpermute needs non-negative tokens and rows and a positive top");
+    if (call->layout != UNISERVE_UNPERMUTE_LAYOUT_PERMUTED && call->layout != UNISERVE_UNPERMUTE_LAYOUT_EXPANDED)
+      return UNISERVE_REFUSE(call, "moe_unpermute's layout is neither permuted nor expanded");
+    if (call->layout == UNISERVE_UNPERMUTE_LAYOUT_EXPANDED && call->routes_rows < call->tokens * call->top)
+      return UNISERVE_REFUSE(call, "moe_unpermute's expanded rows cannot hold every route");
+    if (call->tokens == 0) return 0;
+    if (call->tokens > 0x7fffffffLL)
+      return UNISERVE_REFUSE(call, "moe_unpermute's token count exceeds one grid axis");
+
+    CombineParams p{call->routes, call->out, call->expanded_to_permuted, call->scales,
+                    call->top,    call->hidden, call->routes_rows,
+                    call->layout == UNISERVE_UNPERMUTE_LAYOUT_EXPANDED ? 1 : 0};
+    const dim3 grid(static_cast<uint32_t>(call->tokens),
+                    static_cast<uint32_t>(ceil_div<int64_t>(call->hidden, kColumnsPerBlock)));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (call->input_dtype == UNISERVE_DTYPE_BF16) {
+      if (call->scales_dtype == UNISERVE_DTYPE_F32)
+        hipLaunchKernelGGL((combine_kernel<uint16_t, float>), grid, dim3(kCombineThreads), 0, s, p);
+      else if (call->scales_dtype == UNISERVE_DTYPE_BF16)
+        hipLaunchKernelGGL((combine_kernel<uint16_t, uint16_t>), grid, dim3(kCombineThreads), 0, s, p);
+      else
+        return UNISERVE_REFUSE(call, "moe_unpermute serves bf16 routes with f32 or bf16 scales");
+    } else if (call->input_dtype == UNISERVE_DTYPE_F16) {
+      if (call->scales_dtype == UNISERVE_DTYPE_F32)
+        hipLaunchKernelGGL((combine_kernel<_Float16, float>), grid, dim3(kCombineThreads), 0, s, p);
+      else if (call->scales_dtype == UNISERVE_DTYPE_F16)
+        hipLaunchKernelGGL((combine_kernel<_Float16, _Float16>), grid, dim3(kCombineThreads), 0, s, p);
+      else
+        return UNISERVE_REFUSE(call, "moe_unpermute serves f16 routes with f32 or f16 scales");
+    } else {
+      return UNISERVE_REFUSE(call, "moe_unpermute serves bf16 or f16 routes");
+    }
+    return launched(call, "moe_unpermute");
+  });
+}

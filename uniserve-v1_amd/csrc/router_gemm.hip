@@ -1,0 +1,122 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The router's scores on gfx950 MFMA: scores[m, n] = alpha * x[m, :] . W[n, :] (+ bias[n]), FP32
+// accumulation and one rounding into bf16 - the router `Linear` of the MoE block
+// (crates/nn/src/modules/moe.rs:656-671), which the reference runs as its cuBLASLt `gemm` module
+// (crates/ops/kernels/gemm/cublas_lt, entry `uniserve_gemm`).
+//
+// 64 x 64 output tiles, 64-deep K steps through XOR-swizzled LDS. Weight rows are MFMA operand A
+// and token rows operand B, so each lane holds four consecutive expert scores of one token.
+#include "common.hpp"
+#include "router_gemm.hpp"
+#include "uniserve_gemm.h"
+
+namespace uniserve {
+namespace {
+
+constexpr int kRouterThreads = 256;
+constexpr int kBM = 64, kBN = 64, kBK = 64;
+
+__device__ __forceinline__ int swizzled(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+__global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) {
+  __shared__ u32x4 shared_x[kBM * 8];
+  __shared__ u32x4 shared_w[kBN * 8];
+  const int t = static_cast<int>(threadIdx.x);
+  const int wave = t / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kBN;
+
+  const int chunk = t & 7;
+  const uint16_t *x_row[2];
+  const uint16_t *w_row[2];
+  bool x_valid[2], w_valid[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (t >> 3) + 32 * i;
+    x_valid[i] = m0 + r < p.m;
+    w_valid[i] = n0 + r < p.n;
+    x_row[i] = p.x + (x_valid[i] ? m0 + r : 0) * p.x_stride + chunk * 8;
+    w_row[i] = p.w + (w_valid[i] ? n0 + r : 0) * p.w_stride + chunk * 8;
+  }
+  floatx4 acc[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) acc[ni] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int64_t k0 = 0; k0 < p.k; k0 += kBK) {
+    u32x4 sx[2], sw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      sx[i] = x_valid[i] ? *reinterpret_cast<const u32x4 *>(x_row[i] + k0) : u32x4{0, 0, 0, 0};
+      sw[i] = w_valid[i] ? *reinterpret_cast<const u32x4 *>(w_row[i] + k0) : u32x4{0, 0, 0, 0};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (t >> 3) + 32 * i;
+      shared_x[swizzled(r, chunk)] = sx[i];
+      shared_w[swizzled(r, chunk)] = sw[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + g;
+      const u32x4 xf = shared_x[swizzled(wave * 16 + r16, c)];
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        const u32x4 wf = shared_w[swizzled(ni * 16 + r16, c)];
+        acc[ni] = mfma_16x16x32_bf16(wf, xf, acc[ni]);
+      }
+    }
+  }
+
+  const int64_t m = m0 + wave * 16 + r16;
+  if (m >= p.m) return;
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    const int64_t n = n0 + ni * 16 + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (n + i >= p.n) continue;
+      float v = p.alpha * acc[ni][i];
+      if (p.bias != nullptr) v += p.bias[n + i];
+      p.out[m * p.out_stride + n + i] = f32_to_bf16(v);
+    }
+  }
+}
+
+}  // namespace
+
+void launch_router(const RouterParams &p, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.m, kBM)),
+                  static_cast<uint32_t>(ceil_div<int64_t>(p.n, kBN)));
+  hipLaunchKernelGGL(router_kernel, grid, dim3(kRouterThreads), 0, stream, p);
+}
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_gemm(UniserveGemmCall *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->out == nullptr || call->input == nullptr || call->weight == nullptr)
+      return UNISERVE_REFUSE(call, "gemm needs out, input and weight");
+    if (call->bias != nullptr)
+      return UNISERVE_REFUSE(call, "gemm: this module is compiled without a bias epilogue");
+    if (call->m < 0 || call->n <= 0 || call->k <= 0)
+      return UNISERVE_REFUSE(call, "gemm needs non-negative m and positive n and k");
+    if (call->k % 64 != 0) return UNISERVE_REFUSE(call, "gemm needs a contraction of whole 64-element steps");
+    if (call->input_row_stride < call->k || call->weight_row_stride < call->k || call->out_row_stride < call->n)
+      return UNISERVE_REFUSE(call, "gemm's row strides are shorter than its rows");
+    if (call->input_row_stride % 8 != 0 || call->weight_row_stride % 8 != 0)
+      return UNISERVE_REFUSE(call, "gemm needs 16-byte aligned input and weight rows");
+    if (call->m == 0) return 0;
+    RouterParams p{static_cast<const uint16_t *>(call->input), static_cast<const uint16_t *>(call->weight),
+                   static_cast<uint16_t *>(call->out), nullptr, call->m, call->n, call->k,
+                   call->input_row_stride, call->weight_row_stride, call->out_row_stride, call->alpha};
+    launch_router(p, static_cast<hipStream_t>(stream));
+    return launched(call, "gemm");
+  });
+}
