@@ -29,7 +29,10 @@
 //
 // The dot products over K use a permutation of K that both operands share (lane group g of a
 // 128-element chunk holds elements 32g..32g+31), which changes only the FP32 summation order.
+#include <cstdlib>
+
 #include "common.hpp"
+#include "grouped_tiled.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_route_gemm.h"
 
@@ -300,8 +303,30 @@ __global__ void __launch_bounds__(kThreads) tiled_kernel(GroupedParams p) {
 /// The stream kernel serves batches whose experts average fewer rows than this.
 constexpr int64_t kStreamRowsPerExpert = 24;
 
+/// The staged-DMA tiled kernel serves FC1 widths of whole 128-column slices (FC2: widths % 4).
+template <bool kGated>
+bool staged_fits(const GroupedParams &p) {
+  return (kGated ? p.out_width % 128 == 0 : p.out_width % 4 == 0) && (p.K * 2) % 128 == 0;
+}
+
 template <bool kGated>
 void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, hipStream_t s) {
+  if (!stream_path && staged_fits<kGated>(p)) {
+    TiledParams t{};
+    t.act = p.act;
+    t.weights = p.weights;
+    t.out = p.out;
+    t.tile_to_expert = p.tile_to_expert;
+    t.tile_to_limit = p.tile_to_limit;
+    t.permuted_to_expanded = p.permuted_to_expanded;
+    t.num_tiles = p.num_tiles;
+    t.K = p.K;
+    t.n_total = p.n_total;
+    t.out_width = p.out_width;
+    t.top = p.top;
+    launch_tiled<kGated>(t, max_tiles, s);
+    return;
+  }
   if (stream_path) {
     const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
     hipLaunchKernelGGL(stream_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),

@@ -11,6 +11,8 @@
 // into the FP32 accumulator times s_w * s_x - the per-block dequantisation never touches the
 // operands. The kernels mirror the bf16 ones (`stream` for decode, `tiled` for prefill); the
 // quantiser's codes are bit-exact with the host rule (nearest even, saturating at 448).
+#include <cstdlib>
+
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "uniserve_moe_fp8.h"
