@@ -5,8 +5,12 @@
 // (crates/nn/src/modules/moe.rs:656-671), which the reference runs as its cuBLASLt `gemm` module
 // (crates/ops/kernels/gemm/cublas_lt, entry `uniserve_gemm`).
 //
-// 64 x 64 output tiles, 64-deep K steps through XOR-swizzled LDS. Weight rows are MFMA operand A
-// and token rows operand B, so each lane holds four consecutive expert scores of one token.
+// Two kernels. Batches large enough to fill the chip with 64 x 64 output tiles take 64-deep K
+// steps through XOR-swizzled LDS. Smaller ones (decode: 64 tokens x 128 experts is two such
+// tiles) use 16 x 16 tiles whose contraction is split over the eight wavefronts of a workgroup:
+// each wave loads its K steps straight into registers, four steps in flight, and the partial
+// sums meet in LDS in wave order. In both, weight rows are MFMA operand A and token rows
+// operand B, so each lane holds four consecutive expert scores of one token.
 #include "common.hpp"
 #include "router_gemm.hpp"
 #include "uniserve_gemm.h"
@@ -88,9 +92,69 @@ __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) 
   }
 }
 
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyUnroll = 4;
+
+__global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_router_kernel(RouterParams p) {
+  __shared__ floatx4 partial[kSkinnyWaves][kWave];
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 16 + r16;
+  const int64_t n = static_cast<int64_t>(blockIdx.y) * 16 + r16;
+  // Rows past the edge read row 0 and are never stored.
+  const uint16_t *x_row = p.x + (m < p.m ? m : 0) * p.x_stride + g * 8;
+  const uint16_t *w_row = p.w + (n < p.n ? n : 0) * p.w_stride + g * 8;
+
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t steps = p.k / 32;
+  for (int64_t s = wave; s < steps; s += kSkinnyWaves * kSkinnyUnroll) {
+    u32x4 xv[kSkinnyUnroll], wv[kSkinnyUnroll];
+#pragma unroll
+    for (int u = 0; u < kSkinnyUnroll; ++u) {
+      const int64_t step = s + u * kSkinnyWaves;
+      if (step < steps) {
+        xv[u] = *reinterpret_cast<const u32x4 *>(x_row + step * 32);
+        wv[u] = *reinterpret_cast<const u32x4 *>(w_row + step * 32);
+      } else {
+        xv[u] = u32x4{0, 0, 0, 0};
+        wv[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSkinnyUnroll; ++u) acc = mfma_16x16x32_bf16(wv[u], xv[u], acc);
+  }
+  partial[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  floatx4 total = partial[0][lane];
+#pragma unroll
+  for (int w = 1; w < kSkinnyWaves; ++w) total += partial[w][lane];
+
+  // Lane l holds token r16 and experts 4 g .. 4 g + 3 of the tile.
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + r16;
+  if (row >= p.m) return;
+  const int64_t col = static_cast<int64_t>(blockIdx.y) * 16 + 4 * g;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (col + i >= p.n) continue;
+    float v = p.alpha * total[i];
+    if (p.bias != nullptr) v += p.bias[col + i];
+    p.out[row * p.out_stride + col + i] = f32_to_bf16(v);
+  }
+}
+
 }  // namespace
 
 void launch_router(const RouterParams &p, hipStream_t stream) {
+  // Fewer 64 x 64 tiles than a quarter of the CUs: the split-contraction kernel.
+  const int64_t wide_tiles = ceil_div<int64_t>(p.m, kBM) * ceil_div<int64_t>(p.n, kBN);
+  if (wide_tiles < 64 && p.k % 32 == 0) {
+    const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.m, 16)), static_cast<uint32_t>(ceil_div<int64_t>(p.n, 16)));
+    hipLaunchKernelGGL(skinny_router_kernel, grid, dim3(kSkinnyWaves * kWave), 0, stream, p);
+    return;
+  }
   const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.m, kBM)),
                   static_cast<uint32_t>(ceil_div<int64_t>(p.n, kBN)));
   hipLaunchKernelGGL(router_kernel, grid, dim3(kRouterThreads), 0, stream, p);
