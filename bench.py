@@ -46,6 +46,9 @@ def parse():
     parser.add_argument("--extra", action="store_true", help="also measure every other BASELINE config")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     parser.add_argument("--cpu-runs", type=int, default=3)
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run a plain elementwise copy of 1 GiB in, 1 GiB out (five launches): the "
+                             "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counter readings")
     return parser.parse_args()
 
 
@@ -227,6 +230,16 @@ def cpu_baseline(w, runs):
                       f"OpenMP over {threads} threads"}
 
 
+def measured_traffic(name):
+    """HBM bytes per gather_gemm launch for this config, from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy kernel of known size), or None."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get("configs", {}).get(name, {}).get("gather_gemm")
+    return None if entry is None else entry["hbm_bytes"]
+
+
 def run_config(name, steps, warmup, with_cpu, cpu_runs):
     w = Workload(name)
     elapsed, kernel_ms = measure(w, steps, warmup)
@@ -238,13 +251,13 @@ def run_config(name, steps, warmup, with_cpu, cpu_runs):
     if decode:
         achieved = alg["fc1_bytes"] / fc1_s / 1e9
         roofline = {"kernel": "gather_gemm (FC1 + SiLU)", "bound": "hbm", "achieved": round(achieved, 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(name),
                     "avg_launch_us": round(kernel_ms["gather_gemm"] * 1e3, 2)}
     else:
         achieved = alg["fc1_flops"] / fc1_s / 1e12
         peak = MFMA_PEAK_TFLOPS[w.wdtype]
         roofline = {"kernel": "gather_gemm (FC1 + SiLU)", "bound": "mfma", "achieved": round(achieved, 1),
-                    "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+                    "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": measured_traffic(name),
                     "avg_launch_us": round(kernel_ms["gather_gemm"] * 1e3, 2)}
     layer = {
         "ms_per_step": round(ms_per_step, 4),
@@ -269,6 +282,16 @@ def main():
                           "Run with --gpus 1."}))
         sys.exit(2)
     import torch
+
+    if args.copy_calibration:
+        source = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        target = torch.empty_like(source)
+        for _ in range(5):
+            torch.neg(source, out=target)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": {"bytes_read": source.numel() * 4, "bytes_written": target.numel() * 4,
+                                               "launches": 5, "kernel": "elementwise neg"}}))
+        return
 
     w, ms_per_step, tokens_per_s, roofline, layer, cpu = run_config(
         args.config, args.steps, args.warmup, not args.no_cpu, args.cpu_runs)
