@@ -32,6 +32,7 @@
 #include <cstdlib>
 
 #include "common.hpp"
+#include "grouped_prefill.hpp"
 #include "grouped_tiled.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_route_gemm.h"
@@ -311,6 +312,30 @@ bool staged_fits(const GroupedParams &p) {
 
 template <bool kGated>
 void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, hipStream_t s) {
+  static const int variant = [] {
+    const char *v = std::getenv("UNISERVE_PREFILL");
+    return v == nullptr ? 0 : std::atoi(v);
+  }();
+  if (!stream_path && variant == 0 && prefill_fits<prefill::Bf16, kGated>(p.K, p.out_width)) {
+    PrefillParams q{};
+    q.act = reinterpret_cast<const uint8_t *>(p.act);
+    q.weights = reinterpret_cast<const uint8_t *>(p.weights);
+    q.out = p.out;
+    q.tile_to_expert = p.tile_to_expert;
+    q.tile_to_limit = p.tile_to_limit;
+    q.permuted_to_expanded = p.permuted_to_expanded;
+    q.num_tiles = p.num_tiles;
+    q.K = p.K;
+    q.n_total = p.n_total;
+    q.out_width = p.out_width;
+    q.top = p.top;
+    static const int group = [] {
+      const char *v = std::getenv("UNISERVE_GROUP");
+      return v == nullptr ? 16 : std::atoi(v);
+    }();
+    launch_prefill<prefill::Bf16, kGated>(q, max_tiles, s, group);
+    return;
+  }
   if (!stream_path && staged_fits<kGated>(p)) {
     TiledParams t{};
     t.act = p.act;

@@ -15,6 +15,7 @@
 
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "grouped_prefill.hpp"
 #include "uniserve_moe_fp8.h"
 
 namespace uniserve {
@@ -392,6 +393,35 @@ void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float 
 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
                         hipStream_t stream) {
+  static const int variant = [] {
+    const char *v = std::getenv("UNISERVE_PREFILL");
+    return v == nullptr ? 0 : std::atoi(v);
+  }();
+  const bool fits = gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
+                          : prefill_fits<prefill::E4m3, false>(p.K, p.out_width);
+  if (!stream_path && variant == 0 && fits) {
+    PrefillParams q{};
+    q.act = p.act;
+    q.act_scales = p.act_scales;
+    q.weights = p.weights;
+    q.weight_scales = p.weight_scales;
+    q.out = p.out;
+    q.tile_to_expert = p.tile_to_expert;
+    q.tile_to_limit = p.tile_to_limit;
+    q.permuted_to_expanded = p.permuted_to_expanded;
+    q.num_tiles = p.num_tiles;
+    q.K = p.K;
+    q.n_total = p.n_total;
+    q.out_width = p.out_width;
+    q.top = p.top;
+    static const int group = [] {
+      const char *v = std::getenv("UNISERVE_GROUP");
+      return v == nullptr ? 16 : std::atoi(v);
+    }();
+    if (gated) launch_prefill<prefill::E4m3, true>(q, max_tiles, stream, group);
+    else launch_prefill<prefill::E4m3, false>(q, max_tiles, stream, group);
+    return;
+  }
   const int64_t slices = gated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
   const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices));
   if (stream_path) {
