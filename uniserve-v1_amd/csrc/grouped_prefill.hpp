@@ -173,6 +173,18 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
   const int r32 = lane & 31;
   const int64_t row_bytes = p.K * (F::kScaled ? 1 : 2);
   const int stages = static_cast<int>(row_bytes / 128);
+  // The activation row behind tile row r: FC1 gathers token permuted_to_expanded / top (the maps
+  // are read unconditionally - they span every tile - and padding rows take row 0), FC2 reads its
+  // own permuted row (padding rows read the tile's first row).
+  const int top = static_cast<int>(p.top);
+  auto source_row = [&](int r) -> int64_t {
+    if constexpr (kGated) {
+      const int expanded = p.permuted_to_expanded[first + r];
+      return r < rows ? static_cast<int64_t>(expanded / top) : 0;
+    } else {
+      return r < rows ? first + r : first;
+    }
+  };
 
   // ---- DMA sources: instruction i of this wave fills 8 whole LDS rows; lane l brings logical
   // chunk (l % 8) ^ key(row) of row 8 i' + l / 8, landing in physical chunk l % 8 ----
@@ -182,13 +194,7 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
 #pragma unroll
   for (int i = 0; i < kActLoads; ++i) {
     const int r = (wave * kActLoads + i) * 8 + lane / 8;
-    int64_t source = 0;
-    if (r < rows) {
-      if constexpr (kGated) source = p.permuted_to_expanded[first + r] / p.top;
-      else source = first + r;
-    } else if constexpr (!kGated) {
-      source = first;
-    }
+    const int64_t source = source_row(r);
     a_off[i] = static_cast<uint32_t>(source * row_bytes + ((lane & 7) ^ key(r)) * 16);
   }
   // This wave's 64 weight rows (LDS rows 64 w ..): FC1 rows 0..31 are up rows, 32..63 the gate
@@ -232,13 +238,7 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
   if constexpr (F::kScaled) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      const int m = mi * 32 + r32;
-      int64_t source = first;
-      if (m < rows) {
-        if constexpr (kGated) source = p.permuted_to_expanded[first + m] / p.top;
-        else source = first + m;
-      }
-      sx_row[mi] = static_cast<int>(source) * kb_count;
+      sx_row[mi] = static_cast<int>(source_row(mi * 32 + r32)) * kb_count;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -305,8 +305,8 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
 
   // ---- the K loop (an even number of stages): stage k + 1's DMA and activation scales fly while
   // stage k multiplies. Each wave waits for its own loads, then the barrier for every wave, so
-  // the stage is complete and the other buffer is free to refill. The DMA of the last stage re-reads it (unconditional issue keeps the
-  // waits exact). ----
+  // the stage is complete and the other buffer is free to refill. The DMA of the last stage
+  // re-reads it (unconditional issue keeps the waits exact). ----
   issue(stage0, 0);
   load_scales(0, 0);
   for (int k = 0; k < stages; k += 2) {
@@ -322,13 +322,21 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
     compute(stage1, k + 1, 1);
   }
 
-  // ---- epilogue: lane holds token row 32 mi + lane % 32 and, of block j, weight rows
-  // 8 q + 4 h + i in element 4 q + i ----
+  // ---- epilogue: the output tile goes through LDS so the global stores are whole rows. Lane holds
+  // token row 32 mi + lane % 32 and, of block j, weight rows 8 q + 4 h + i in element 4 q + i.
+  // LDS rows are padded to kOutStride bytes (8 more than a multiple of 256), so the
+  // 32 rows one 8-byte write instruction touches fall on distinct banks. Rows 0..63 live in the
+  // first stage buffer, rows 64..127 in the second. ----
+  constexpr int kOutCols = slice_width<kGated>();
+  constexpr int kOutStride = kOutCols * 2 + 8;
+  static_assert(64 * kOutStride <= static_cast<int>(sizeof(Stage)), "the output tile fits the stage buffers");
+  auto out_row = [&](int m) -> char * {
+    return (m < 64 ? reinterpret_cast<char *>(&stage0) : reinterpret_cast<char *>(&stage1)) + (m & 63) * kOutStride;
+  };
+  __syncthreads();  // every wave is done reading the stage buffers
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
-    const int m = mi * 32 + r32;
-    if (m >= rows) continue;
-    uint16_t *row = p.out + (first + m) * p.out_width;
+    char *row = out_row(mi * 32 + r32);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       if constexpr (kGated) {
@@ -338,25 +346,36 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
         uint2 packed;
         packed.x = pack_bf16x2(v[0], v[1]);
         packed.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2 *>(row + wave_col + 8 * q + 4 * h) = packed;
+        *reinterpret_cast<uint2 *>(row + (wave * 32 + 8 * q + 4 * h) * 2) = packed;
       } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if (!block_live[j]) continue;
           uint2 packed;
           packed.x = pack_bf16x2(acc[mi][j][4 * q], acc[mi][j][4 * q + 1]);
           packed.y = pack_bf16x2(acc[mi][j][4 * q + 2], acc[mi][j][4 * q + 3]);
-          *reinterpret_cast<uint2 *>(row + weight_row(j) + 8 * q + 4 * h) = packed;
+          *reinterpret_cast<uint2 *>(row + (wave * 64 + j * 32 + 8 * q + 4 * h) * 2) = packed;
         }
       }
     }
+  }
+  __syncthreads();
+  // Write-out: 16-byte pieces, consecutive lanes along a row; live rows and columns only.
+  constexpr int kPieces = kOutCols / 8;
+  const int64_t live_cols = min(static_cast<int64_t>(kOutCols), p.out_width - slice_col);
+  for (int index = t; index < kRows * kPieces; index += kThreads) {
+    const int m = index / kPieces;
+    const int c = index - m * kPieces;
+    if (m >= rows || c * 8 >= live_cols) continue;
+    const u32x4 piece = *reinterpret_cast<const u32x4 *>(out_row(m) + c * 16);
+    *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
   }
 }
 
 }  // namespace prefill
 
 /// Whether the prefill kernel serves this shape: an even number of 128-byte K stages, FC1 widths
-/// of whole 256-column slices, FC2 widths of whole 32-row blocks (e4m3: whole 128-row scale blocks).
+/// of whole 256-column slices, FC2 widths of whole 32-row blocks (e4m3: whole 128-row scale blocks);
+/// FC2 widths that are a multiple of 8 columns keep the epilogue's 16-byte pieces whole.
 template <class F, bool kGated>
 inline bool prefill_fits(int64_t K, int64_t out_width) {
   const int64_t row_bytes = K * (F::kScaled ? 1 : 2);
