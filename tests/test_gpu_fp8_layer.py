@@ -226,3 +226,41 @@ def test_layer_is_deterministic(device):
     a = bf16_bits(layer(x, router, up_gate, down)).copy()
     b = bf16_bits(layer(x, router, up_gate, down))
     np.testing.assert_array_equal(a, b)
+
+
+def test_prefill_fc1_quantises_like_the_quantiser(device):
+    """At prefill shapes the layer's FC1 writes the gated rows straight in FC2's e4m3 form; codes
+    and scales of every live row equal the stand-alone FC1 (bf16 out) followed by quantize_fp8."""
+    announce("fused FC1 quantisation")
+    tokens, hidden, experts, top, intermediate = 2048, 2048, 128, 8, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 40)
+    q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+    q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+    w1, w2 = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+    ws1, ws2 = torch.from_numpy(s1).to(device), torch.from_numpy(s2).to(device)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f8e4m3")
+    layer(x, router, w1, w2, up_gate_scales=ws1, down_scales=ws2)
+    torch.cuda.synchronize()
+    rows = layer.views.permuted_rows
+    fused_q = layer.view("gated_q", torch.uint8, (rows, intermediate)).cpu().numpy()
+    fused_s = layer.view("gated_s", torch.float32, (rows, intermediate // 128)).cpu().numpy()
+
+    class Maps:
+        def __getitem__(self, index):
+            name = ["tile_to_expert", "tile_to_limit", "expanded_to_permuted", "permuted_to_expanded",
+                    "permuted_to_token", "total_padded_tokens", "num_non_exiting_tiles"][index]
+            length = {0: layer.views.max_tiles, 1: layer.views.max_tiles, 2: tokens * top, 3: rows, 4: rows,
+                      5: 1, 6: 1}[index]
+            return layer.view(name, torch.int32, (length,))
+
+    xq = layer.view("hidden_q", torch.uint8, (tokens, hidden))
+    xs = layer.view("hidden_s", torch.float32, (tokens, hidden // 128))
+    gated = ops.gather_gemm_fp8(xq, xs, w1, ws1, top, Maps(), rows)
+    want_q, want_s = ops.quantize_fp8(gated)
+    torch.cuda.synchronize()
+    p2e = layer.view("permuted_to_expanded", torch.int32, (rows,)).cpu().numpy()
+    padded = int(layer.view("total_padded_tokens", torch.int32, (1,)).cpu().numpy()[0])
+    live = np.nonzero(p2e[:padded] >= 0)[0]
+    assert live.size == tokens * top
+    np.testing.assert_array_equal(fused_q[live], want_q.cpu().numpy()[live])
+    np.testing.assert_array_equal(fused_s[live].view(np.uint32), want_s.cpu().numpy()[live].view(np.uint32))

@@ -8,7 +8,50 @@
 
 #include <cstdint>
 
+#include "common.hpp"
+#include "uniserve_moe_fp8.h"
+
 namespace uniserve {
+
+// ---- e4m3 encoding ---------------------------------------------------------------------------------------
+
+/// Nearest-even e4m3fn code of `value`, saturating at +-448 (0x7e); NaN -> 0x7f.
+__device__ __forceinline__ uint32_t e4m3_encode(float value) {
+  const uint32_t bits = __float_as_uint(value);
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const float a = __builtin_fabsf(value);
+  if (a != a) return sign | 0x7fu;
+  if (a >= 448.0f) return sign | 0x7eu;
+  if (a < 0.015625f) return sign | static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
+  const int e = static_cast<int>((__float_as_uint(a) >> 23) & 0xffu) - 127;
+  const float unit = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);  // 2^-e, exact
+  int m = static_cast<int>(__builtin_rintf((a * unit - 1.0f) * 8.0f));
+  int exponent = e;
+  if (m == 8) {
+    m = 0;
+    exponent += 1;
+  }
+  uint32_t code = static_cast<uint32_t>(((exponent + 7) << 3) | m);
+  if (code > 0x7eu) code = 0x7eu;
+  return sign | code;
+}
+
+/// The e4m3 codes of a pair of quotients, packed into the low 16 bits. gfx950's conversion rounds
+/// to nearest even exactly as e4m3_encode does wherever |q| <= 448 (checked over every such
+/// float); anything else (saturation, NaN) takes e4m3_encode.
+__device__ __forceinline__ uint32_t e4m3_pair(float q0, float q1) {
+  if (__builtin_fabsf(q0) <= 448.0f && __builtin_fabsf(q1) <= 448.0f)
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0, false)) & 0xffffu;
+  return e4m3_encode(q0) | (e4m3_encode(q1) << 8);
+}
+
+/// Eight bf16-rounded values quantised with one scale: their e4m3 codes, packed low to high.
+__device__ __forceinline__ uint2 e4m3_eight(const float (&v)[8], float scale) {
+  uint2 out;
+  out.x = e4m3_pair(v[0] / scale, v[1] / scale) | (e4m3_pair(v[2] / scale, v[3] / scale) << 16);
+  out.y = e4m3_pair(v[4] / scale, v[5] / scale) | (e4m3_pair(v[6] / scale, v[7] / scale) << 16);
+  return out;
+}
 
 struct GroupedFp8Params {
   const uint8_t *act;           ///< FC1: hidden [tokens, K]; FC2: rows [permuted_rows, K], e4m3
@@ -24,6 +67,8 @@ struct GroupedFp8Params {
   int64_t n_total;
   int64_t out_width;
   int64_t top;
+  uint8_t *out_codes;           ///< FC1 only, or null: the gated rows as e4m3 [permuted_rows, out_width]
+  float *out_code_scales;       ///< with out_codes: [permuted_rows, out_width / 128]
 };
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
@@ -31,5 +76,14 @@ void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
                         hipStream_t stream);
 bool fp8_stream_path(int64_t routes, int64_t experts);
+
+/// Whether FC1 in e4m3 can write its gated rows already quantised for FC2 (the prefill kernel
+/// serves the shape), which spares the layer the bf16 round trip and the separate quantiser.
+bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate);
+
+/// The gather_gemm_fp8 entry; with `codes` (and `code_scales`) set, the gated rows are written as
+/// e4m3 codes and per-128-column scales - bit for bit what uniserve_quantize_fp8 makes of the bf16
+/// rows - instead of bf16 (refused unless fp8_fc1_quantizes).
+int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales, void *stream);
 
 }  // namespace uniserve

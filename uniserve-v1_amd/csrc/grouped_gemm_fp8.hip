@@ -20,29 +20,6 @@
 
 namespace uniserve {
 
-// ---- e4m3 encoding ---------------------------------------------------------------------------------------
-
-/// Nearest-even e4m3fn code of `value`, saturating at +-448 (0x7e); NaN -> 0x7f.
-__device__ __forceinline__ uint32_t e4m3_encode(float value) {
-  const uint32_t bits = __float_as_uint(value);
-  const uint32_t sign = (bits >> 24) & 0x80u;
-  const float a = __builtin_fabsf(value);
-  if (a != a) return sign | 0x7fu;
-  if (a >= 448.0f) return sign | 0x7eu;
-  if (a < 0.015625f) return sign | static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
-  const int e = static_cast<int>((__float_as_uint(a) >> 23) & 0xffu) - 127;
-  const float unit = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);  // 2^-e, exact
-  int m = static_cast<int>(__builtin_rintf((a * unit - 1.0f) * 8.0f));
-  int exponent = e;
-  if (m == 8) {
-    m = 0;
-    exponent += 1;
-  }
-  uint32_t code = static_cast<uint32_t>(((exponent + 7) << 3) | m);
-  if (code > 0x7eu) code = 0x7eu;
-  return sign | code;
-}
-
 namespace {
 
 // ---- the activation quantiser -------------------------------------------------------------------------------
@@ -95,13 +72,7 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
   for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
   if (!active) return;
   const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    lo |= e4m3_encode(v[j] / scale) << (8 * j);
-    hi |= e4m3_encode(v[j + 4] / scale) << (8 * j);
-  }
-  *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = make_uint2(lo, hi);
+  *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, scale);
   if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
 }
 
@@ -414,6 +385,8 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.n_total = p.n_total;
     q.out_width = p.out_width;
     q.top = p.top;
+    q.out_codes = p.out_codes;
+    q.out_code_scales = p.out_code_scales;
     static const int group = [] {
       const char *v = std::getenv("UNISERVE_GROUP");
       return v == nullptr ? 16 : std::atoi(v);
@@ -455,8 +428,13 @@ extern "C" int32_t uniserve_quantize_fp8(const uniserve_quantize_fp8_call *call,
   });
 }
 
-extern "C" int32_t uniserve_gather_gemm_fp8(const uniserve_gather_fp8_call *call, void *stream) {
-  using namespace uniserve;
+namespace uniserve {
+
+bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate) {
+  return !fp8_stream_path(tokens * top, experts) && prefill_fits<prefill::E4m3, true>(hidden_size, intermediate);
+}
+
+int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_fp8 writes bf16 only");
     if (call->block_n != 128 || call->block_k != 128)
@@ -492,10 +470,22 @@ extern "C" int32_t uniserve_gather_gemm_fp8(const uniserve_gather_fp8_call *call
     p.n_total = call->width;
     p.out_width = call->width / 2;
     p.top = call->top;
+    if (codes != nullptr) {
+      if (!fp8_fc1_quantizes(call->tokens, call->top, call->experts, call->hidden_size, call->width / 2))
+        return UNISERVE_REFUSE(call, "gather_gemm_fp8 quantises its output only on the prefill kernel's shapes");
+      p.out_codes = codes;
+      p.out_code_scales = code_scales;
+    }
     launch_grouped_fp8(p, true, max_tiles, fp8_stream_path(call->tokens * call->top, call->experts),
                        static_cast<hipStream_t>(stream));
     return launched(call, "gather_gemm_fp8");
   });
+}
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_gather_gemm_fp8(const uniserve_gather_fp8_call *call, void *stream) {
+  return uniserve::gather_gemm_fp8(call, nullptr, nullptr, stream);
 }
 
 extern "C" int32_t uniserve_route_gemm_fp8(const uniserve_route_fp8_call *call, void *stream) {

@@ -34,6 +34,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "grouped_fp8.hpp"
 
 namespace uniserve {
 
@@ -55,6 +56,8 @@ struct PrefillParams {
   int32_t max_tiles;
   int32_t group;                 ///< tiles per work group of the numbering
   int32_t per_xcd;               ///< work items per XCD range
+  uint8_t *out_codes;            ///< FC1 only, or null: write the gated rows as e4m3 codes
+  float *out_code_scales;        ///< with out_codes: [permuted_rows, out_width / 128]
 };
 
 namespace prefill {
@@ -359,6 +362,36 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
     }
   }
   __syncthreads();
+  if (kGated && p.out_codes != nullptr) {
+    // Write-out as the FC2 operand: each (row, 128-column group) is quantised by 16 lanes from the
+    // bf16 values in LDS (the same rounding points and encoding as the stand-alone quantiser:
+    // amax of the bf16 values, s = amax / 448, code = e4m3(v / s)), live rows only.
+    constexpr int kGroups = kOutCols / 128;
+    const int sub = t & 15;
+    const int64_t groups_per_row = p.out_width / 128;
+    for (int index = t / 16; index < kRows * kGroups; index += kThreads / 16) {
+      const int m = index / kGroups;
+      const int group = index - m * kGroups;
+      const u32x4 piece = *reinterpret_cast<const u32x4 *>(out_row(m) + (group * 128 + sub * 8) * 2);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(piece[j] << 16);
+        v[2 * j + 1] = __uint_as_float(piece[j] & 0xffff0000u);
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+#pragma unroll
+      for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+      if (m >= rows) continue;
+      const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+      const int64_t column = slice_col + group * 128 + sub * 8;
+      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(v, scale);
+      if (sub == 0) p.out_code_scales[(first + m) * groups_per_row + column / 128] = scale;
+    }
+    return;
+  }
   // Write-out: 16-byte pieces, consecutive lanes along a row; live rows and columns only.
   constexpr int kPieces = kOutCols / 8;
   const int64_t live_cols = min(static_cast<int64_t>(kOutCols), p.out_width - slice_col);

@@ -227,7 +227,14 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       fc1.block_k = 128;
       fc1.out_dtype = UNISERVE_DTYPE_BF16;
       fc1.multiprocessors = call->multiprocessors;
-      if (uniserve_gather_gemm_fp8(&fc1, stream) != 0) return forward_error(call, "gather_gemm_fp8", fc1);
+      const bool fused = fp8_fc1_quantizes(call->tokens, call->top, call->experts, call->hidden_size, call->intermediate);
+      if (fused) {
+        // Prefill shapes: FC1 writes the gated rows straight in FC2's e4m3 form.
+        if (gather_gemm_fp8(&fc1, static_cast<uint8_t *>(at(v.gated_q)), static_cast<float *>(at(v.gated_s)), stream) != 0)
+          return forward_error(call, "gather_gemm_fp8", fc1);
+      } else if (uniserve_gather_gemm_fp8(&fc1, stream) != 0) {
+        return forward_error(call, "gather_gemm_fp8", fc1);
+      }
 
       uniserve_quantize_fp8_call qg{};
       qg.input = at(v.gated);
@@ -238,7 +245,7 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       qg.width = call->intermediate;
       qg.input_dtype = UNISERVE_DTYPE_BF16;
       qg.group = 128;
-      if (uniserve_quantize_fp8(&qg, stream) != 0) return forward_error(call, "quantize_fp8", qg);
+      if (!fused && uniserve_quantize_fp8(&qg, stream) != 0) return forward_error(call, "quantize_fp8", qg);
 
       uniserve_route_fp8_call fc2{};
       fc2.rows = at(v.gated_q);

@@ -177,6 +177,201 @@ __global__ void __launch_bounds__(kSortThreads) moe_sort_kernel(SortParams p) {
   }
 }
 
+// ---- the split path: more routes than one workgroup places ------------------------------------------
+//
+// Three launches over chunks of kSplitChunk routes (the last chunk also takes the remainder, so
+// every chunk holds at least twice as many routes as there are local experts):
+//   count: each chunk's held routes per expert, parked at the head of the chunk's own stretch of
+//          `expanded_to_permuted` (which only that chunk's placement overwrites later);
+//   scan:  one workgroup turns the parked counts into in-expert offsets, parks the experts' first
+//          rows right after them, and writes the tile tables, the padding rows and the two counts;
+//   place: each chunk reads its first rows back, then places its routes in order.
+// Every launch is wide (one workgroup per chunk) or tiny, instead of one pass that recounts all
+// routes per workgroup.
+
+constexpr int kSplitThreads = 512;
+constexpr int kSplitWaves = kSplitThreads / kWave;
+constexpr int64_t kSplitChunk = 2048;
+
+__device__ __forceinline__ void split_chunk(const SortParams &p, int64_t *first, int64_t *past) {
+  const int64_t chunks = p.routes / kSplitChunk;
+  *first = static_cast<int64_t>(blockIdx.x) * kSplitChunk;
+  *past = static_cast<int64_t>(blockIdx.x) + 1 == chunks ? p.routes : *first + kSplitChunk;
+}
+
+/// Per-wavefront counts of the held routes of [first, past): wavefront w takes the w-th contiguous
+/// slice of whole 64-route groups (so a later in-order walk of the slices is stable), counting into
+/// its own row of `wave_rows` ([kSplitWaves][E], zero on entry).
+__device__ __forceinline__ void split_count(const SortParams &p, int64_t first, int64_t past, int64_t live,
+                                            int32_t *wave_rows, int64_t *slice_first, int64_t *slice_past) {
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t groups = (past - first + kWave - 1) / kWave;
+  const int64_t own = (groups + kSplitWaves - 1) / kSplitWaves;
+  *slice_first = first + static_cast<int64_t>(wave) * own * kWave;
+  *slice_past = *slice_first + own * kWave < past ? *slice_first + own * kWave : past;
+  int32_t *mine = wave_rows + wave * p.local_experts;
+  constexpr int kGroups = 8;  // the wave's ids loads in flight together
+  for (int64_t base = *slice_first; base < *slice_past; base += kGroups * kWave) {
+    int32_t e[kGroups];
+#pragma unroll
+    for (int u = 0; u < kGroups; ++u) {
+      const int64_t route = base + u * kWave + lane;
+      e[u] = route < *slice_past ? local_expert(p, route, live) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kGroups; ++u) {
+      const uint64_t peers = match_any(static_cast<uint32_t>(e[u] + 1), p.key_bits);
+      if (e[u] >= 0 && (peers & below) == 0) mine[e[u]] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kSplitThreads) sort_count_kernel(SortParams p) {
+  extern __shared__ int32_t lds[];
+  const int E = p.local_experts;
+  int32_t *wave_rows = lds;  // [kSplitWaves][E]
+  for (int i = threadIdx.x; i < kSplitWaves * E; i += kSplitThreads) wave_rows[i] = 0;
+  __syncthreads();
+  const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
+  int64_t first, past, slice_first, slice_past;
+  split_chunk(p, &first, &past);
+  split_count(p, first, past, live, wave_rows, &slice_first, &slice_past);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kSplitThreads) {
+    int32_t sum = 0;
+    for (int w = 0; w < kSplitWaves; ++w) sum += wave_rows[w * E + e];
+    p.expanded_to_permuted[first + e] = sum;
+  }
+}
+
+__global__ void __launch_bounds__(kSortThreads) sort_scan_kernel(SortParams p) {
+  extern __shared__ int32_t lds[];
+  const int E = p.local_experts;
+  int32_t *total = lds;             // [E]
+  int32_t *first_row = total + E;   // [E]
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int64_t chunks = p.routes / kSplitChunk;
+  constexpr int kBatchChunks = 16;
+
+  // Each expert's running count over the chunks; the parked counts become in-expert offsets.
+  for (int e = threadIdx.x; e < E; e += kSortThreads) {
+    int32_t running = 0;
+    for (int64_t c0 = 0; c0 < chunks; c0 += kBatchChunks) {
+      int32_t count[kBatchChunks];
+#pragma unroll
+      for (int u = 0; u < kBatchChunks; ++u)
+        count[u] = c0 + u < chunks ? p.expanded_to_permuted[(c0 + u) * kSplitChunk + e] : 0;
+#pragma unroll
+      for (int u = 0; u < kBatchChunks; ++u) {
+        if (c0 + u < chunks) p.expanded_to_permuted[(c0 + u) * kSplitChunk + e] = running;
+        running += count[u];
+      }
+    }
+    total[e] = running;
+  }
+  __syncthreads();
+
+  // Each expert's first tile: an exclusive scan of the tile counts by the first wavefront.
+  if (wave == 0) {
+    int32_t carried = 0;
+    for (int base = 0; base < E; base += kWave) {
+      const int e = base + lane;
+      const int32_t tiles = e < E ? (total[e] + p.tile - 1) / p.tile : 0;
+      int32_t inclusive = tiles;
+#pragma unroll
+      for (int offset = 1; offset < kWave; offset *= 2) {
+        const int32_t other = __shfl_up(inclusive, offset);
+        if (lane >= offset) inclusive += other;
+      }
+      if (e < E) first_row[e] = (carried + inclusive - tiles) * p.tile;
+      carried += __shfl(inclusive, kWave - 1);
+    }
+    if (lane == 0) {
+      p.total_padded_tokens[0] = carried * p.tile;
+      p.num_non_exiting_tiles[0] = carried;
+    }
+  }
+  __syncthreads();
+
+  // Tile tables and the padding rows of each expert's last tile, one wavefront per expert.
+  for (int e = wave; e < E; e += kSortWaves) {
+    const int32_t count = total[e];
+    if (count == 0) continue;
+    const int32_t first = first_row[e];
+    const int32_t tiles = (count + p.tile - 1) / p.tile;
+    const int32_t first_tile = first / p.tile;
+    for (int32_t t = lane; t < tiles; t += kWave) {
+      const int32_t end_of_tile = (first_tile + t + 1) * p.tile;
+      const int32_t end_of_rows = first + count;
+      p.tile_to_expert[first_tile + t] = e;
+      p.tile_to_limit[first_tile + t] = end_of_tile < end_of_rows ? end_of_tile : end_of_rows;
+    }
+    for (int32_t row = count + lane; row < tiles * p.tile; row += kWave) {
+      p.permuted_to_expanded[first + row] = -1;
+      p.permuted_to_token[first + row] = -1;
+    }
+  }
+
+  // Each chunk also gets the experts' first rows, parked right after its offsets (stores only).
+  for (int64_t i = threadIdx.x; i < chunks * E; i += kSortThreads) {
+    const int64_t c = i / E;
+    const int e = static_cast<int>(i - c * E);
+    p.expanded_to_permuted[c * kSplitChunk + E + e] = first_row[e];
+  }
+}
+
+__global__ void __launch_bounds__(kSplitThreads) sort_place_kernel(SortParams p) {
+  extern __shared__ int32_t lds[];
+  const int E = p.local_experts;
+  int32_t *start = lds;              // [E]
+  int32_t *wave_rows = start + E;    // [kSplitWaves][E]
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
+  int64_t first, past, slice_first, slice_past;
+  split_chunk(p, &first, &past);
+  // The chunk's first rows (expert first row plus the chunk's offset, both parked in the chunk's
+  // own slots) are read before any of its routes is written over them.
+  for (int e = threadIdx.x; e < E; e += kSplitThreads)
+    start[e] = p.expanded_to_permuted[first + e] + p.expanded_to_permuted[first + E + e];
+  for (int i = threadIdx.x; i < kSplitWaves * E; i += kSplitThreads) wave_rows[i] = 0;
+  __syncthreads();
+  split_count(p, first, past, live, wave_rows, &slice_first, &slice_past);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kSplitThreads) {
+    int32_t running = start[e];
+    for (int w = 0; w < kSplitWaves; ++w) {
+      const int32_t count = wave_rows[w * E + e];
+      wave_rows[w * E + e] = running;
+      running += count;
+    }
+  }
+  __syncthreads();
+  int32_t *mine = wave_rows + wave * E;
+  for (int64_t base = slice_first; base < slice_past; base += kWave) {
+    const int64_t route = base + lane;
+    const bool inside = route < slice_past;
+    const int32_t e = inside ? local_expert(p, route, live) : -1;
+    const uint64_t peers = match_any(static_cast<uint32_t>(e + 1), p.key_bits);
+    if (e >= 0) {
+      const int32_t row = mine[e] + __popcll(peers & below);
+      p.expanded_to_permuted[route] = row;
+      p.permuted_to_expanded[row] = static_cast<int32_t>(route);
+      p.permuted_to_token[row] = static_cast<int32_t>(route / p.top);
+    } else if (inside) {
+      p.expanded_to_permuted[route] = route < live ? -1 : -2;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0 && (peers & below) == 0) mine[e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 }  // namespace
 }  // namespace uniserve
 
@@ -222,9 +417,19 @@ extern "C" int32_t uniserve_moe_sort(const uniserve_moe_sort_call *call, void *s
     int bits = 0;
     while ((1ll << bits) <= call->local_experts) ++bits;
     p.key_bits = bits;
-    const int64_t chunks = p.routes == 0 ? 1 : ceil_div<int64_t>(p.routes, kChunk);
-    hipLaunchKernelGGL(moe_sort_kernel, dim3(static_cast<uint32_t>(chunks)), dim3(kSortThreads),
-                       static_cast<size_t>(lds_bytes), static_cast<hipStream_t>(stream), p);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p.routes <= kChunk || 2 * p.local_experts > kSplitChunk) {
+      const int64_t chunks = p.routes == 0 ? 1 : ceil_div<int64_t>(p.routes, kChunk);
+      hipLaunchKernelGGL(moe_sort_kernel, dim3(static_cast<uint32_t>(chunks)), dim3(kSortThreads),
+                         static_cast<size_t>(lds_bytes), s, p);
+      return launched(call, "moe_sort");
+    }
+    const uint32_t chunks = static_cast<uint32_t>(p.routes / kSplitChunk);
+    const size_t count_bytes = kSplitWaves * call->local_experts * sizeof(int32_t);
+    hipLaunchKernelGGL(sort_count_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes, s, p);
+    hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kSortThreads), 2 * call->local_experts * sizeof(int32_t), s, p);
+    hipLaunchKernelGGL(sort_place_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes + call->local_experts * sizeof(int32_t),
+                       s, p);
     return launched(call, "moe_sort");
   });
 }

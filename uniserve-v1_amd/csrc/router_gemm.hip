@@ -6,7 +6,7 @@
 // (crates/ops/kernels/gemm/cublas_lt, entry `uniserve_gemm`).
 //
 // Two kernels. Batches large enough to fill the chip with 64 x 64 output tiles take 64-deep K
-// steps through XOR-swizzled LDS. Smaller ones (decode: 64 tokens x 128 experts is two such
+// steps through two XOR-swizzled LDS buffers, their loads eight steps ahead in registers. Smaller ones (decode: 64 tokens x 128 experts is two such
 // tiles) use 16 x 16 tiles whose contraction is split over the eight wavefronts of a workgroup:
 // each wave loads its K steps straight into registers, four steps in flight, and the partial
 // sums meet in LDS in wave order. In both, weight rows are MFMA operand A and token rows
@@ -20,12 +20,13 @@ namespace {
 
 constexpr int kRouterThreads = 256;
 constexpr int kBM = 64, kBN = 64, kBK = 64;
+constexpr int kDepth = 8;  // K steps whose loads are in flight
 
 __device__ __forceinline__ int swizzled(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
 
 __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) {
-  __shared__ u32x4 shared_x[kBM * 8];
-  __shared__ u32x4 shared_w[kBN * 8];
+  __shared__ u32x4 shared_x[2][kBM * 8];
+  __shared__ u32x4 shared_w[2][kBN * 8];
   const int t = static_cast<int>(threadIdx.x);
   const int wave = t / kWave;
   const int lane = lane_id();
@@ -50,29 +51,44 @@ __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) 
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) acc[ni] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int64_t k0 = 0; k0 < p.k; k0 += kBK) {
-    u32x4 sx[2], sw[2];
+  // The K steps' global loads run kDepth steps ahead in registers (the MFMA work of a step is far
+  // shorter than a load's latency); each step goes through one of two LDS buffers, one barrier
+  // per step.
+  const int64_t steps = p.k / kBK;
+  u32x4 rx[kDepth][2], rw[kDepth][2];
+  auto load = [&](int d, int64_t step) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      sx[i] = x_valid[i] ? *reinterpret_cast<const u32x4 *>(x_row[i] + k0) : u32x4{0, 0, 0, 0};
-      sw[i] = w_valid[i] ? *reinterpret_cast<const u32x4 *>(w_row[i] + k0) : u32x4{0, 0, 0, 0};
+      rx[d][i] = x_valid[i] ? *reinterpret_cast<const u32x4 *>(x_row[i] + step * kBK) : u32x4{0, 0, 0, 0};
+      rw[d][i] = w_valid[i] ? *reinterpret_cast<const u32x4 *>(w_row[i] + step * kBK) : u32x4{0, 0, 0, 0};
     }
-    __syncthreads();
+  };
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = (t >> 3) + 32 * i;
-      shared_x[swizzled(r, chunk)] = sx[i];
-      shared_w[swizzled(r, chunk)] = sw[i];
-    }
-    __syncthreads();
+  for (int d = 0; d < kDepth; ++d)
+    if (d < steps) load(d, d);
+  for (int64_t k0 = 0; k0 < steps; k0 += kDepth) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int c = ks * 4 + g;
-      const u32x4 xf = shared_x[swizzled(wave * 16 + r16, c)];
+    for (int d = 0; d < kDepth; ++d) {
+      const int64_t k = k0 + d;
+      if (k >= steps) break;
+      const int buffer = static_cast<int>(k & 1);
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) {
-        const u32x4 wf = shared_w[swizzled(ni * 16 + r16, c)];
-        acc[ni] = mfma_16x16x32_bf16(wf, xf, acc[ni]);
+      for (int i = 0; i < 2; ++i) {
+        const int r = (t >> 3) + 32 * i;
+        shared_x[buffer][swizzled(r, chunk)] = rx[d][i];
+        shared_w[buffer][swizzled(r, chunk)] = rw[d][i];
+      }
+      __syncthreads();
+      if (k + kDepth < steps) load(d, k + kDepth);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int c = ks * 4 + g;
+        const u32x4 xf = shared_x[buffer][swizzled(wave * 16 + r16, c)];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+          const u32x4 wf = shared_w[buffer][swizzled(ni * 16 + r16, c)];
+          acc[ni] = mfma_16x16x32_bf16(wf, xf, acc[ni]);
+        }
       }
     }
   }
