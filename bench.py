@@ -46,6 +46,9 @@ def parse():
     parser.add_argument("--extra", action="store_true", help="also measure every other BASELINE config")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     parser.add_argument("--cpu-runs", type=int, default=3)
+    parser.add_argument("--traffic-summary", metavar="DIR",
+                        help="only fold rocprofv3 FETCH_SIZE / WRITE_SIZE passes (DIR/<config>/{fetch,write}, "
+                             "DIR/calibration/{fetch,write}, csv) into profiles/hbm_traffic.json")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain elementwise copy of 1 GiB in, 1 GiB out (five launches): the "
                              "known-size reference for scaling FETCH_SIZE / WRITE_SIZE counter readings")
@@ -240,6 +243,60 @@ def measured_traffic(name):
     return None if entry is None else entry["hbm_bytes"]
 
 
+def counter_means(directory, counter):
+    """Mean per-dispatch value of `counter` per kernel name, over every counter CSV under `directory`."""
+    import csv
+
+    sums, counts = {}, {}
+    for path in Path(directory).rglob("*counter_collection.csv"):
+        with open(path) as handle:
+            for row in csv.DictReader(handle):
+                if row["Counter_Name"] != counter:
+                    continue
+                key = row["Kernel_Name"]
+                sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
+                counts[key] = counts.get(key, 0) + 1
+    return {key: sums[key] / counts[key] for key in sums}
+
+
+def traffic_summary(directory):
+    """HBM bytes per launch of the grouped products of each config: FETCH_SIZE and WRITE_SIZE (KiB
+    per dispatch) scaled so that a plain copy of 1 GiB in / 1 GiB out reads exactly its bytes."""
+    root = Path(directory)
+    calib_fetch = max(counter_means(root / "calibration" / "fetch", "FETCH_SIZE").values())
+    calib_write = max(counter_means(root / "calibration" / "write", "WRITE_SIZE").values())
+    gib_kib = float(1 << 20)
+    fetch_scale, write_scale = gib_kib / calib_fetch, gib_kib / calib_write
+    import re
+
+    products = {"gather_gemm": "true", "route_gemm": "false"}
+    pattern = re.compile(r"((?:stream|prefill)\w*)<([^<>]*)>\(")
+    configs = {}
+    for name in CONFIGS:
+        if not (root / name).exists():
+            continue
+        fetch = counter_means(root / name / "fetch", "FETCH_SIZE")
+        write = counter_means(root / name / "write", "WRITE_SIZE")
+        entry = {}
+        for product, gated in products.items():
+            found = [(k, m) for k, m in ((k, pattern.search(k)) for k in fetch) if m and m.group(2).endswith(gated)]
+            if not found:
+                continue
+            kernel, match = found[0]
+            f, wr = fetch[kernel], write.get(kernel, 0.0)
+            entry[product] = {"kernel": f"{match.group(1)}<{match.group(2).replace('uniserve::', '')}>",
+                              "fetch_KiB": round(f, 1),
+                              "write_KiB": round(wr, 1),
+                              "hbm_bytes": int(f * 1024 * fetch_scale + wr * 1024 * write_scale)}
+        configs[name] = entry
+    summary = {"method": "rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE (KiB per dispatch, averaged over the "
+                         "run's dispatches of the kernel), scaled by the readings for a plain elementwise copy of "
+                         "1 GiB in / 1 GiB out (bench.py --copy-calibration)",
+               "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4), "configs": configs}
+    (ROOT / "profiles" / "hbm_traffic.json").write_text(json.dumps(summary, indent=1) + "\n")
+    print(json.dumps(summary))
+
+
 def run_config(name, steps, warmup, with_cpu, cpu_runs):
     w = Workload(name)
     elapsed, kernel_ms = measure(w, steps, warmup)
@@ -281,6 +338,9 @@ def main():
                           "holds all experts on it (expert-parallel sharding is a design note, not a path). "
                           "Run with --gpus 1."}))
         sys.exit(2)
+    if args.traffic_summary:
+        traffic_summary(args.traffic_summary)
+        return
     import torch
 
     if args.copy_calibration:
