@@ -1,0 +1,215 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The router's per-token routine (softmax, top-k, renormalisation, scale, map, load), shared by
+// the topk_softmax kernel and the layer's fused route-and-sort kernel.
+//
+// One token per 32-lane half of a 64-lane wavefront. The probabilities are FP32 reductions whose
+// rounding depends on their order, and the selection compares them for equality, so the routine
+// keeps the reference's reduction tree exactly (crates/ops/kernels/topk_softmax/nvcc/src/
+// topk_softmax.cu:106-199): lane j of a half holds experts j + 32 i, sums its own terms in i
+// order, and the halves exchange by xor butterflies over 16, 8, 4, 2, 1 within the half (DPP quad
+// permutes for 1 and 2, ds_swizzle bit-mask mode for 4, 8 and 16).
+//
+// The exponential is the library's own (`router_expf`) and not the platform's, so that the CPU
+// oracle evaluates the identical operations: every probability, and therefore every id, is
+// reproducible bit for bit on the host.
+#pragma once
+
+#include <cfloat>
+#include <climits>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace uniserve {
+namespace topk {
+
+constexpr int kHalf = 32;
+
+/// Cody-Waite reduction x = n ln2 + r and the degree-7 Taylor polynomial of e^r (Horner, fused
+/// multiply-adds), scaled by 2^n in two exact power-of-two steps.
+__device__ __forceinline__ float router_expf(float x) {
+  if (x != x) return x;
+  if (x < -104.0f) return 0.0f;
+  if (x > 88.75f) return __builtin_inff();
+  const float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int k = static_cast<int>(n);
+  const int half = k / 2;
+  const float first = __uint_as_float(static_cast<uint32_t>(half + 127) << 23);
+  const float second = __uint_as_float(static_cast<uint32_t>(k - half + 127) << 23);
+  return (p * first) * second;
+}
+
+/// The value of lane (this lane xor kOffset), within each 32-lane half.
+template <int kOffset>
+__device__ __forceinline__ int xor_lane(int value) {
+  if constexpr (kOffset == 1) {
+    return __builtin_amdgcn_mov_dpp(value, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (kOffset == 2) {
+    return __builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else {
+    // Bit-mask swizzle over 32 lanes: and 0x1f, or 0, xor kOffset.
+    return __builtin_amdgcn_ds_swizzle(value, (kOffset << 10) | 0x1F);
+  }
+}
+
+template <int kOffset>
+__device__ __forceinline__ float xor_lane(float value) {
+  return __int_as_float(xor_lane<kOffset>(__float_as_int(value)));
+}
+
+__device__ __forceinline__ float load_kind(const void *data, int kind, int64_t index) {
+  if (kind == 0) return static_cast<const float *>(data)[index];
+  if (kind == 2) return static_cast<float>(static_cast<const _Float16 *>(data)[index]);
+  return bf16_to_f32(static_cast<const uint16_t *>(data)[index]);
+}
+
+template <int kOffset>
+__device__ __forceinline__ void max_step(float &maximum) {
+  const float other = xor_lane<kOffset>(maximum);
+  maximum = maximum < other ? other : maximum;
+}
+
+template <int kOffset>
+__device__ __forceinline__ void sum_step(float &sum) {
+  sum = sum + xor_lane<kOffset>(sum);
+}
+
+template <int kOffset>
+__device__ __forceinline__ void argmax_step(float &best, int &expert) {
+  const float other = xor_lane<kOffset>(best);
+  const int other_expert = xor_lane<kOffset>(expert);
+  if (other > best || (other == best && other_expert < expert)) {
+    best = other;
+    expert = other_expert;
+  }
+}
+
+/// Routes one token with `kIter` scores per lane (the expert count in whole halves, rounded up to
+/// a power of two: the extra slots hold -inf and add exact zeros to the sum).
+template <int kIter>
+__device__ __forceinline__ void route(const void *scores, int score_kind, int64_t row_stride,
+                                      int row, int experts, int top, int renormalize,
+                                      const void *scale, int scale_kind, int32_t *ids,
+                                      float *weights, const int32_t *map, const int32_t *live,
+                                      unsigned long long *load, bool active) {
+  const int lane = static_cast<int>(threadIdx.x) & (kHalf - 1);
+  float values[kIter];
+#pragma unroll
+  for (int it = 0; it < kIter; ++it) {
+    const int expert = lane + it * kHalf;
+    values[it] = expert < experts
+                     ? load_kind(scores, score_kind, static_cast<int64_t>(row) * row_stride + expert)
+                     : -__builtin_inff();
+  }
+
+  float maximum = values[0];
+#pragma unroll
+  for (int it = 0; it < kIter; ++it) maximum = maximum > values[it] ? maximum : values[it];
+  max_step<16>(maximum);
+  max_step<8>(maximum);
+  max_step<4>(maximum);
+  max_step<2>(maximum);
+  max_step<1>(maximum);
+
+  float sum = 0.0f;
+#pragma unroll
+  for (int it = 0; it < kIter; ++it) {
+    values[it] = router_expf(values[it] - maximum);
+    sum += values[it];
+  }
+  sum_step<16>(sum);
+  sum_step<8>(sum);
+  sum_step<4>(sum);
+  sum_step<2>(sum);
+  sum_step<1>(sum);
+#pragma unroll
+  for (int it = 0; it < kIter; ++it) values[it] = values[it] / sum;
+
+  // `top` rounds of a (value, lower id) arg-max; lane j keeps round j's pick.
+  float picked = 0.0f;
+  int picked_expert = 0;
+  uint32_t taken = 0u;
+  for (int j = 0; j < top; ++j) {
+    float best = -1.0f;
+    int best_expert = INT_MAX;
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int expert = lane + it * kHalf;
+      if (expert < experts && !((taken >> it) & 1u) && values[it] > best) {
+        best = values[it];
+        best_expert = expert;
+      }
+    }
+    argmax_step<16>(best, best_expert);
+    argmax_step<8>(best, best_expert);
+    argmax_step<4>(best, best_expert);
+    argmax_step<2>(best, best_expert);
+    argmax_step<1>(best, best_expert);
+    if (lane == j) {
+      picked = best;
+      picked_expert = best_expert;
+    }
+    // A round that named no expert (a row of NaN scores) marks nothing taken.
+    if (best_expert >= 0 && best_expert < experts && (best_expert & (kHalf - 1)) == lane)
+      taken |= 1u << (best_expert / kHalf);
+  }
+
+  float weight = picked;
+  if (renormalize) {
+    // The butterfly over the next power of two of `top` lanes, lanes past `top` holding zero.
+    int width = 1;
+    while (width < top) width *= 2;
+    float partial = lane < top ? picked : 0.0f;
+    if (width > 16) sum_step<16>(partial);
+    if (width > 8) sum_step<8>(partial);
+    if (width > 4) sum_step<4>(partial);
+    if (width > 2) sum_step<2>(partial);
+    if (width > 1) sum_step<1>(partial);
+    const float total = partial < FLT_EPSILON ? FLT_EPSILON : partial;
+    weight = weight / total;
+  }
+  if (!active || lane >= top) return;
+  const bool named = picked_expert >= 0 && picked_expert < experts;
+  if (scale_kind != -1 && scale != nullptr && named) weight = weight * load_kind(scale, scale_kind, picked_expert);
+  const int64_t slot = static_cast<int64_t>(row) * top + lane;
+  ids[slot] = (map != nullptr && named) ? map[picked_expert] : picked_expert;
+  weights[slot] = weight;
+  if (load != nullptr && named && (live == nullptr || row < live[0])) atomicAdd(load + picked_expert, 1ull);
+}
+
+
+/// Routes token `row` (`active` false: take part in the wavefront's exchanges, store nothing),
+/// with the per-lane slot count the expert count needs.
+__device__ __forceinline__ void route_token(const void *scores, int score_kind, int64_t row_stride, int row,
+                                            int experts, int top, int renormalize, const void *scale,
+                                            int scale_kind, int32_t *ids, float *weights, const int32_t *map,
+                                            const int32_t *live, unsigned long long *load, bool active) {
+  const int needed = (experts + kHalf - 1) / kHalf;
+  if (needed <= 1)
+    route<1>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+  else if (needed <= 2)
+    route<2>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+  else if (needed <= 4)
+    route<4>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+  else if (needed <= 8)
+    route<8>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+  else if (needed <= 16)
+    route<16>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+  else
+    route<32>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+}
+
+}  // namespace topk
+}  // namespace uniserve
