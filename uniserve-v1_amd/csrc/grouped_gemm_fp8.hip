@@ -96,10 +96,15 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
 }
 
 constexpr int kPassTiles = 2;
+constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is split over the waves
 
-/// Decode-shaped: as the bf16 stream kernel, one 128-deep scale block per chunk.
-template <bool kGated>
+/// Decode-shaped: as the bf16 stream kernel, one 128-deep scale block per chunk. kSplit: the four
+/// wavefronts share one row set and split K (scale block kb goes to wave kb % 4), their partial sums
+/// meeting in LDS in wave order - four times the workgroups, for batches whose tiles x slices would
+/// leave most of the chip idle (a single token: 8 tiles).
+template <bool kGated, bool kSplit>
 __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p) {
+  __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   const int tile = static_cast<int>(blockIdx.x);
   if (tile >= p.num_tiles[0]) return;
   const int64_t expert = p.tile_to_expert[tile];
@@ -112,14 +117,17 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   const int64_t kb_count = p.K / 128;
 
   int64_t n0, n1;
+  const int row_set = kSplit ? 0 : wave;
   if constexpr (kGated) {
-    n0 = static_cast<int64_t>(blockIdx.y) * 64 + wave * 16;
+    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 16 : 64) + row_set * 16;
     n1 = p.out_width + n0;
   } else {
-    n0 = static_cast<int64_t>(blockIdx.y) * 128 + wave * 32;
+    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
     n1 = n0 + 16;
     if (n0 >= p.out_width) return;
   }
+  const int64_t kb_first = kSplit ? wave : 0;
+  const int64_t kb_step = kSplit ? kThreads / kWave : 1;
   const uint8_t *w0 = p.weights + (expert * p.n_total + n0 + r16) * p.K + g * 32;
   const uint8_t *w1 = p.weights + (expert * p.n_total + n1 + r16) * p.K + g * 32;
   const float *ws0 = p.weight_scales + (expert * (p.n_total / 128) + n0 / 128) * kb_count;
@@ -169,12 +177,32 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
           for (int i = 0; i < 4; ++i) acc[set][ms][i] = __builtin_fmaf(block[i], scale, acc[set][ms][i]);
         }
     };
-    fetch(0, wcur, acur, scur);
-    for (int64_t kb = 0; kb < kb_count; kb += 2) {
-      if (kb + 1 < kb_count) fetch(kb + 1, wnext, anext, snext);
+    if (kb_first < kb_count) fetch(kb_first, wcur, acur, scur);
+    for (int64_t kb = kb_first; kb < kb_count; kb += 2 * kb_step) {
+      if (kb + kb_step < kb_count) fetch(kb + kb_step, wnext, anext, snext);
       compute(wcur, acur, scur);
-      if (kb + 2 < kb_count) fetch(kb + 2, wcur, acur, scur);
-      if (kb + 1 < kb_count) compute(wnext, anext, snext);
+      if (kb + 2 * kb_step < kb_count) fetch(kb + 2 * kb_step, wcur, acur, scur);
+      if (kb + kb_step < kb_count) compute(wnext, anext, snext);
+    }
+    if constexpr (kSplit) {
+      // Waves 1..3 hand their partial sums to wave 0, which adds them in wave order.
+      if (wave > 0) {
+#pragma unroll
+        for (int set = 0; set < 2; ++set)
+#pragma unroll
+          for (int ms = 0; ms < kPassTiles; ++ms) partial[wave - 1][set][ms][lane] = acc[set][ms];
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < kThreads / kWave - 1; ++w)
+#pragma unroll
+          for (int set = 0; set < 2; ++set)
+#pragma unroll
+            for (int ms = 0; ms < kPassTiles; ++ms) acc[set][ms] += partial[w][set][ms][lane];
+      }
+      __syncthreads();
+      if (wave > 0) continue;
     }
 
 #pragma unroll
@@ -398,8 +426,17 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
   const int64_t slices = gated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
   const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices));
   if (stream_path) {
-    if (gated) hipLaunchKernelGGL(stream_fp8_kernel<true>, grid, dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL(stream_fp8_kernel<false>, grid, dim3(kThreads), 0, stream, p);
+    // Fewer workgroups than two per CU of a large part: split K over the waves instead.
+    if (max_tiles * slices < kSplitBelow) {
+      const int64_t split_slices = gated ? p.out_width / 16 : ceil_div<int64_t>(p.out_width, 32);
+      const dim3 split_grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(split_slices));
+      if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, true>), split_grid, dim3(kThreads), 0, stream, p);
+      else hipLaunchKernelGGL((stream_fp8_kernel<false, true>), split_grid, dim3(kThreads), 0, stream, p);
+    } else if (gated) {
+      hipLaunchKernelGGL((stream_fp8_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((stream_fp8_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+    }
   } else {
     if (gated) hipLaunchKernelGGL(tiled_fp8_kernel<true>, grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL(tiled_fp8_kernel<false>, grid, dim3(kThreads), 0, stream, p);
