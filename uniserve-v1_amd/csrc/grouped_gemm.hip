@@ -177,6 +177,139 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   }
 }
 
+// ---- line-wise stream kernel ------------------------------------------------------------------------------
+//
+// The decode product again, with the weight stream read as whole 128-byte lines: a load
+// instruction covers 8 rows x 128 bytes (eight lanes per row), marked non-temporal since every
+// weight line is read once per call - which lets HBM run near its streaming rate, where the
+// MFMA-layout loads above consume each line over four instructions. The lines are redistributed
+// into the MFMA operand layout (lane l: row l % 16) with ds_bpermute, which moves data between
+// lanes without allocating LDS. A stage is 256 bytes of K per row (two lines, 128 bf16): eight
+// line loads per wavefront for its 32 weight rows.
+//
+// K mapping (the same for weights and activations): step s in 0..3 of a stage, lane group
+// g = l / 16 takes the stage's 16-byte chunk 4 s + g, i.e. line s / 2, chunk 4 (s % 2) + g.
+
+/// The 16 bytes lane `source` holds in `value`, gathered by this lane.
+__device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
+  u32x4 out;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    out[d] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(source * 4, static_cast<int>(value[d])));
+  return out;
+}
+
+template <bool kGated>
+__global__ void __launch_bounds__(kThreads) stream_lines_kernel(GroupedParams p) {
+  const int tile = static_cast<int>(blockIdx.x);
+  if (tile >= p.num_tiles[0]) return;
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  int64_t n0, n1;
+  if constexpr (kGated) {
+    n0 = static_cast<int64_t>(blockIdx.y) * 64 + wave * 16;
+    n1 = p.out_width + n0;
+  } else {
+    n0 = static_cast<int64_t>(blockIdx.y) * 128 + wave * 32;
+    n1 = n0 + 16;
+    if (n0 >= p.out_width) return;
+  }
+  // Line load i of a stage (i = 0..7): line i / 4 of rows 8 (i % 4) + l / 8 of the wave's 32 (set
+  // 0 = rows n0.., set 1 = rows n1..), 16-byte chunk l % 8.
+  const uint16_t *line_row[2];
+  line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * p.K + (lane & 7) * 8;
+  line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * p.K + (lane & 7) * 8;
+  // Fragment (set, s): lane l takes row r16 of the set from line load 4 (s / 2) + 2 set + r16 / 8,
+  // lane 8 (r16 % 8) + 4 (s % 2) + g.
+  const bool upper = r16 >= 8;
+  const int source0 = (r16 & 7) * 8 + g;      // s even
+  const int source1 = source0 + 4;            // s odd
+  const int stages = static_cast<int>(p.K / 128);
+
+  for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
+    const uint16_t *a[kPassTiles];
+    bool valid[kPassTiles];
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      valid[ms] = m < rows;
+      int64_t source = first + m;
+      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      a[ms] = p.act + (valid[ms] ? source : 0) * p.K + g * 8;
+    }
+    floatx4 acc[2][kPassTiles];
+#pragma unroll
+    for (int set = 0; set < 2; ++set)
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms) acc[set][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    struct Stage {
+      u32x4 lines[8];
+      u32x4 act[kPassTiles][4];
+    };
+    auto load = [&](Stage &st, int64_t k) {
+      const int64_t offset = k * 128;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int set = (i % 4) / 2;
+        const int64_t row_offset = static_cast<int64_t>((i % 4) % 2) * 8 * p.K;
+        st.lines[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(line_row[set] + row_offset + offset + (i / 4) * 64));
+      }
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          st.act[ms][s] = valid[ms] ? load16(a[ms] + offset + s * 32) : u32x4{0, 0, 0, 0};
+    };
+    auto compute = [&](const Stage &st) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int source = (s & 1) ? source1 : source0;
+#pragma unroll
+        for (int set = 0; set < 2; ++set) {
+          const int i = 4 * (s / 2) + 2 * set;
+          const u32x4 lo = permute16(source, st.lines[i]);
+          const u32x4 hi = permute16(source, st.lines[i + 1]);
+          const u32x4 w = upper ? hi : lo;
+#pragma unroll
+          for (int ms = 0; ms < kPassTiles; ++ms) acc[set][ms] = mfma_16x16x32_bf16(w, st.act[ms][s], acc[set][ms]);
+        }
+      }
+    };
+    Stage even, odd;
+    load(even, 0);
+    for (int k = 0; k < stages; k += 2) {
+      if (k + 1 < stages) load(odd, k + 1);
+      compute(even);
+      if (k + 2 < stages) load(even, k + 2);
+      if (k + 1 < stages) compute(odd);
+    }
+
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      if (m >= rows) continue;
+      uint16_t *row = p.out + (first + m) * p.out_width;
+      if constexpr (kGated) {
+        floatx4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        store_bf16x4(row + n0 + 4 * g, h);
+      } else {
+        store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
+        store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
+      }
+    }
+  }
+}
+
 // ---- tiled kernel -----------------------------------------------------------------------------------------
 
 constexpr int kBK = 64;               // K elements per stage: 8 chunks of 16 bytes per row
@@ -354,6 +487,10 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
   }
   if (stream_path) {
     const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
+    if (variant == 0)
+      hipLaunchKernelGGL(stream_lines_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
+                         dim3(kThreads), 0, s, p);
+    else
     hipLaunchKernelGGL(stream_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
                        dim3(kThreads), 0, s, p);
   } else {

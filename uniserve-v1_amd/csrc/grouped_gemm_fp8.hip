@@ -81,12 +81,6 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
 constexpr int kTileRows = 128;
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ intx8 load32(const uint8_t *pointer) {
-  const u32x4 lo = *reinterpret_cast<const u32x4 *>(pointer);
-  const u32x4 hi = *reinterpret_cast<const u32x4 *>(pointer + 16);
-  return intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
-               static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-}
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
   uint2 packed;
@@ -96,6 +90,16 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
 }
 
 constexpr int kPassTiles = 2;
+
+/// The 16 bytes lane `source` holds in `value`, gathered by this lane (ds_bpermute: lanes exchange
+/// registers without LDS allocation).
+__device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
+  u32x4 out;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    out[d] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(source * 4, static_cast<int>(value[d])));
+  return out;
+}
 constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is split over the waves
 
 /// Decode-shaped: as the bf16 stream kernel, one 128-deep scale block per chunk. kSplit: the four
@@ -128,8 +132,17 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   }
   const int64_t kb_first = kSplit ? wave : 0;
   const int64_t kb_step = kSplit ? kThreads / kWave : 1;
-  const uint8_t *w0 = p.weights + (expert * p.n_total + n0 + r16) * p.K + g * 32;
-  const uint8_t *w1 = p.weights + (expert * p.n_total + n1 + r16) * p.K + g * 32;
+  // Weight lines: load i (0..3) of a scale block reads rows 8 (i % 2) + l / 8 of set i / 2 (set 0 =
+  // rows n0.., set 1 = rows n1..), 16-byte chunk l % 8 - whole 128-byte lines, non-temporal (each
+  // weight line is read once per call). Lane l's MFMA operand (row r16, 32 K bytes of group g:
+  // chunks g and g + 4) is gathered from those loads with ds_bpermute; the activations use the
+  // same K mapping.
+  const uint8_t *line_row[2];
+  line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * p.K + (lane & 7) * 16;
+  line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * p.K + (lane & 7) * 16;
+  const bool upper = r16 >= 8;
+  const int source_lo = (r16 & 7) * 8 + g;  // chunk g of row r16
+  const int source_hi = source_lo + 4;      // chunk g + 4
   const float *ws0 = p.weight_scales + (expert * (p.n_total / 128) + n0 / 128) * kb_count;
   const float *ws1 = p.weight_scales + (expert * (p.n_total / 128) + n1 / 128) * kb_count;
 
@@ -144,7 +157,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
       int64_t source = first + m;
       if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
       if (!valid[ms]) source = 0;
-      a[ms] = p.act + source * p.K + g * 32;
+      a[ms] = p.act + source * p.K + g * 16;
       as[ms] = p.act_scales + source * kb_count;
     }
     floatx4 acc[2][kPassTiles];
@@ -153,20 +166,43 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    intx8 wcur[2], wnext[2], acur[kPassTiles], anext[kPassTiles];
+    u32x4 wcur[4], wnext[4];
+    intx8 acur[kPassTiles], anext[kPassTiles];
     float scur[2 + kPassTiles], snext[2 + kPassTiles];
-    auto fetch = [&](int64_t kb, intx8 (&w)[2], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
-      w[0] = load32(w0 + kb * 128);
-      w[1] = load32(w1 + kb * 128);
+    auto fetch = [&](int64_t kb, u32x4 (&w)[4], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * p.K + kb * 128));
       s[0] = ws0[kb];
       s[1] = ws1[kb];
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) {
-        x[ms] = valid[ms] ? load32(a[ms] + kb * 128) : intx8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (valid[ms]) {
+          const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
+          const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
+          x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                        static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+        } else {
+          x[ms] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
         s[2 + ms] = valid[ms] ? as[ms][kb] : 0.0f;
       }
     };
-    auto compute = [&](const intx8 (&w)[2], const intx8 (&x)[kPassTiles], const float (&s)[2 + kPassTiles]) {
+    auto compute = [&](const u32x4 (&lines)[4], const intx8 (&x)[kPassTiles], const float (&s)[2 + kPassTiles]) {
+      intx8 w[2];
+#pragma unroll
+      for (int set = 0; set < 2; ++set) {
+        // Every lane takes part in both permutes of both loads; the select picks its row's load.
+        const u32x4 lo0 = permute16(source_lo, lines[2 * set]);
+        const u32x4 lo1 = permute16(source_lo, lines[2 * set + 1]);
+        const u32x4 hi0 = permute16(source_hi, lines[2 * set]);
+        const u32x4 hi1 = permute16(source_hi, lines[2 * set + 1]);
+        const u32x4 lo = upper ? lo1 : lo0;
+        const u32x4 hi = upper ? hi1 : hi0;
+        w[set] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                       static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+      }
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms)
 #pragma unroll
