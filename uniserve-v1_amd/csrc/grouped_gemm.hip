@@ -11,29 +11,29 @@
 // accumulation, the activation on the accumulators, one rounding into bf16; rows past a tile's
 // limit are neither read nor stored.
 //
-// Two kernels per product, chosen on the host from the expected rows per expert (tokens x top /
-// experts), which is all the host knows without reading device memory:
+// Three kernels per product, chosen on the host from the expected rows per expert (tokens x top /
+// experts), which is all the host knows without reading device memory, and from the shape:
 //
 //  * `stream` (decode: a few rows per expert). Weight-streaming bound: every touched expert's
 //    matrix is read once from HBM and nothing else matters. A workgroup owns one tile and a
-//    128-row slice of the expert's weight rows; each wavefront streams 32 weight rows straight from
-//    HBM into registers (64 contiguous bytes per lane per row, double-buffered, no LDS), and the
-//    tile's activation rows come from L2. The weight rows are MFMA operand A and the activation
-//    rows operand B (16x16x32 bf16), so each lane ends holding four consecutive output columns of
-//    one row - an 8-byte store - and the SiLU pair (up column n, gate column n) meets in one lane.
-//    Tiles of more than 32 rows are covered in passes of 32.
+//    128-row slice of the expert's weight rows; each wavefront streams its 32 weight rows as whole
+//    non-temporal 128-byte lines into registers and regroups them into the MFMA operand layout with
+//    ds_bpermute (no LDS), the tile's activation rows coming from L2. The weight rows are MFMA
+//    operand A and the activation rows operand B (16x16x32 bf16), so each lane ends holding four
+//    consecutive output columns of one row - an 8-byte store - and the SiLU pair (up column n,
+//    gate column n) meets in one lane. Tiles of more than 32 rows are covered in passes of 32.
 //
-//  * `tiled` (prefill: hundreds of rows per expert). MFMA-bound: a 128 x 128 output tile per
+//  * `prefill` (grouped_prefill.hpp; hundreds of rows per expert): 128 x 512 tiles of 8
+//    wavefronts, both operands DMA'd into LDS, for the shapes it serves.
+//
+//  * `tiled` (prefill shapes the prefill kernel does not serve): a 128 x 128 output tile per
 //    workgroup, 64-deep K steps staged through XOR-swizzled LDS (two stages, one barrier per step),
 //    four wavefronts of 64 x 64, global loads of step k + 1 in flight during the MFMAs of step k.
 //
-// The dot products over K use a permutation of K that both operands share (lane group g of a
-// 128-element chunk holds elements 32g..32g+31), which changes only the FP32 summation order.
-#include <cstdlib>
-
+// The dot products over K use a permutation of K that both operands share, which changes only the
+// FP32 summation order.
 #include "common.hpp"
 #include "grouped_prefill.hpp"
-#include "grouped_tiled.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_route_gemm.h"
 
@@ -68,121 +68,19 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
   *reinterpret_cast<uint2 *>(pointer) = packed;
 }
 
-// ---- stream kernel -----------------------------------------------------------------------------------
+// ---- stream kernel (decode) ----------------------------------------------------------------------------
 
 /// Rows of a tile one pass covers: kPassTiles MFMA blocks of 16.
 constexpr int kPassTiles = 2;
 
-template <bool kGated>
-struct StreamChunk {
-  u32x4 w[2][4];             ///< [row set][MFMA K step]
-  u32x4 a[kPassTiles][4];    ///< [16-row block][MFMA K step]
-};
-
-template <bool kGated>
-__device__ __forceinline__ void stream_load(StreamChunk<kGated> &chunk, const uint16_t *w0,
-                                            const uint16_t *w1, const uint16_t *const *a,
-                                            const bool *valid, int64_t offset) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    chunk.w[0][j] = load16(w0 + offset + j * 8);
-    chunk.w[1][j] = load16(w1 + offset + j * 8);
-  }
-#pragma unroll
-  for (int ms = 0; ms < kPassTiles; ++ms)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) chunk.a[ms][j] = valid[ms] ? load16(a[ms] + offset + j * 8) : u32x4{0, 0, 0, 0};
-}
-
-template <bool kGated>
-__device__ __forceinline__ void stream_compute(const StreamChunk<kGated> &chunk,
-                                               floatx4 (&acc)[2][kPassTiles]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int ms = 0; ms < kPassTiles; ++ms) {
-      acc[0][ms] = mfma_16x16x32_bf16(chunk.w[0][j], chunk.a[ms][j], acc[0][ms]);
-      acc[1][ms] = mfma_16x16x32_bf16(chunk.w[1][j], chunk.a[ms][j], acc[1][ms]);
-    }
-}
-
-/// Grid: (max tiles, weight-row slices). FC1 slices are 64 gated columns (64 up + 64 gate rows),
-/// FC2 slices 128 output columns; wavefront w takes 16 + 16 of them. Needs K % 128 == 0.
-template <bool kGated>
-__global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
-  const int tile = static_cast<int>(blockIdx.x);
-  if (tile >= p.num_tiles[0]) return;
-  const int64_t expert = p.tile_to_expert[tile];
-  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
-  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
-  const int lane = lane_id();
-  const int r16 = lane & 15;
-  const int g = lane >> 4;
-
-  int64_t n0, n1;
-  if constexpr (kGated) {
-    n0 = static_cast<int64_t>(blockIdx.y) * 64 + wave * 16;
-    n1 = p.out_width + n0;
-  } else {
-    n0 = static_cast<int64_t>(blockIdx.y) * 128 + wave * 32;
-    n1 = n0 + 16;
-    if (n0 >= p.out_width) return;  // a last slice of 64 columns leaves two wavefronts idle
-  }
-  const uint16_t *w0 = p.weights + (expert * p.n_total + n0 + r16) * p.K + g * 32;
-  const uint16_t *w1 = p.weights + (expert * p.n_total + n1 + r16) * p.K + g * 32;
-  const int chunks = static_cast<int>(p.K / 128);
-
-  for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
-    const uint16_t *a[kPassTiles];
-    bool valid[kPassTiles];
-#pragma unroll
-    for (int ms = 0; ms < kPassTiles; ++ms) {
-      const int m = pass + ms * 16 + r16;
-      valid[ms] = m < rows;
-      int64_t source = first + m;
-      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
-      a[ms] = p.act + (valid[ms] ? source : 0) * p.K + g * 32;
-    }
-    floatx4 acc[2][kPassTiles];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    StreamChunk<kGated> even, odd;
-    stream_load(even, w0, w1, a, valid, 0);
-    for (int c = 0; c < chunks; c += 2) {
-      if (c + 1 < chunks) stream_load(odd, w0, w1, a, valid, static_cast<int64_t>(c + 1) * 128);
-      stream_compute(even, acc);
-      if (c + 2 < chunks) stream_load(even, w0, w1, a, valid, static_cast<int64_t>(c + 2) * 128);
-      if (c + 1 < chunks) stream_compute(odd, acc);
-    }
-
-#pragma unroll
-    for (int ms = 0; ms < kPassTiles; ++ms) {
-      const int m = pass + ms * 16 + r16;
-      if (m >= rows) continue;
-      uint16_t *row = p.out + (first + m) * p.out_width;
-      if constexpr (kGated) {
-        floatx4 h;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
-        store_bf16x4(row + n0 + 4 * g, h);
-      } else {
-        store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
-        store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
-      }
-    }
-  }
-}
-
-// ---- line-wise stream kernel ------------------------------------------------------------------------------
 //
-// The decode product again, with the weight stream read as whole 128-byte lines: a load
-// instruction covers 8 rows x 128 bytes (eight lanes per row), marked non-temporal since every
-// weight line is read once per call - which lets HBM run near its streaming rate, where the
-// MFMA-layout loads above consume each line over four instructions. The lines are redistributed
+// Grid: (max tiles, weight-row slices). FC1 slices are 64 gated columns (64 up + 64 gate rows),
+// FC2 slices 128 output columns; wavefront w takes 16 + 16 of them. Needs K % 128 == 0.
+//
+// The weight stream is read as whole 128-byte lines: a load instruction covers 8 rows x 128 bytes
+// (eight lanes per row), marked non-temporal since every weight line is read once per call - which
+// lets HBM run near its streaming rate (loads in the MFMA operand layout consume each line over
+// four instructions, and reach about 0.70 of the peak against 0.78). The lines are redistributed
 // into the MFMA operand layout (lane l: row l % 16) with ds_bpermute, which moves data between
 // lanes without allocating LDS. A stage is 256 bytes of K per row (two lines, 128 bf16): eight
 // line loads per wavefront for its 32 weight rows.
@@ -200,7 +98,7 @@ __device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
 }
 
 template <bool kGated>
-__global__ void __launch_bounds__(kThreads) stream_lines_kernel(GroupedParams p) {
+__global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   const int tile = static_cast<int>(blockIdx.x);
   if (tile >= p.num_tiles[0]) return;
   const int64_t expert = p.tile_to_expert[tile];
@@ -437,19 +335,9 @@ __global__ void __launch_bounds__(kThreads) tiled_kernel(GroupedParams p) {
 /// The stream kernel serves batches whose experts average fewer rows than this.
 constexpr int64_t kStreamRowsPerExpert = 24;
 
-/// The staged-DMA tiled kernel serves FC1 widths of whole 128-column slices (FC2: widths % 4).
-template <bool kGated>
-bool staged_fits(const GroupedParams &p) {
-  return (kGated ? p.out_width % 128 == 0 : p.out_width % 4 == 0) && (p.K * 2) % 128 == 0;
-}
-
 template <bool kGated>
 void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, hipStream_t s) {
-  static const int variant = [] {
-    const char *v = std::getenv("UNISERVE_PREFILL");
-    return v == nullptr ? 0 : std::atoi(v);
-  }();
-  if (!stream_path && variant == 0 && prefill_fits<prefill::Bf16, kGated>(p.K, p.out_width)) {
+  if (!stream_path && prefill_fits<prefill::Bf16, kGated>(p.K, p.out_width)) {
     PrefillParams q{};
     q.act = reinterpret_cast<const uint8_t *>(p.act);
     q.weights = reinterpret_cast<const uint8_t *>(p.weights);
@@ -462,42 +350,13 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
     q.n_total = p.n_total;
     q.out_width = p.out_width;
     q.top = p.top;
-    static const int group = [] {
-      const char *v = std::getenv("UNISERVE_GROUP");
-      return v == nullptr ? 16 : std::atoi(v);
-    }();
-    launch_prefill<prefill::Bf16, kGated>(q, max_tiles, s, group);
+    launch_prefill<prefill::Bf16, kGated>(q, max_tiles, s);
     return;
   }
-  if (!stream_path && staged_fits<kGated>(p)) {
-    TiledParams t{};
-    t.act = p.act;
-    t.weights = p.weights;
-    t.out = p.out;
-    t.tile_to_expert = p.tile_to_expert;
-    t.tile_to_limit = p.tile_to_limit;
-    t.permuted_to_expanded = p.permuted_to_expanded;
-    t.num_tiles = p.num_tiles;
-    t.K = p.K;
-    t.n_total = p.n_total;
-    t.out_width = p.out_width;
-    t.top = p.top;
-    launch_tiled<kGated>(t, max_tiles, s);
-    return;
-  }
-  if (stream_path) {
-    const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
-    if (variant == 0)
-      hipLaunchKernelGGL(stream_lines_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
-                         dim3(kThreads), 0, s, p);
-    else
-    hipLaunchKernelGGL(stream_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
-                       dim3(kThreads), 0, s, p);
-  } else {
-    const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
-    hipLaunchKernelGGL(tiled_kernel<kGated>, dim3(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices)),
-                       dim3(kThreads), 0, s, p);
-  }
+  const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
+  const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices));
+  if (stream_path) hipLaunchKernelGGL(stream_kernel<kGated>, grid, dim3(kThreads), 0, s, p);
+  else hipLaunchKernelGGL(tiled_kernel<kGated>, grid, dim3(kThreads), 0, s, p);
 }
 
 }  // namespace

@@ -11,8 +11,6 @@
 // into the FP32 accumulator times s_w * s_x - the per-block dequantisation never touches the
 // operands. The kernels mirror the bf16 ones (`stream` for decode, `tiled` for prefill); the
 // quantiser's codes are bit-exact with the host rule (nearest even, saturating at 448).
-#include <cstdlib>
-
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_prefill.hpp"
@@ -428,13 +426,9 @@ void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float 
 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
                         hipStream_t stream) {
-  static const int variant = [] {
-    const char *v = std::getenv("UNISERVE_PREFILL");
-    return v == nullptr ? 0 : std::atoi(v);
-  }();
   const bool fits = gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
                           : prefill_fits<prefill::E4m3, false>(p.K, p.out_width);
-  if (!stream_path && variant == 0 && fits) {
+  if (!stream_path && fits) {
     PrefillParams q{};
     q.act = p.act;
     q.act_scales = p.act_scales;
@@ -451,12 +445,8 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.top = p.top;
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
-    static const int group = [] {
-      const char *v = std::getenv("UNISERVE_GROUP");
-      return v == nullptr ? 16 : std::atoi(v);
-    }();
-    if (gated) launch_prefill<prefill::E4m3, true>(q, max_tiles, stream, group);
-    else launch_prefill<prefill::E4m3, false>(q, max_tiles, stream, group);
+    if (gated) launch_prefill<prefill::E4m3, true>(q, max_tiles, stream);
+    else launch_prefill<prefill::E4m3, false>(q, max_tiles, stream);
     return;
   }
   const int64_t slices = gated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
