@@ -62,37 +62,42 @@ struct PrefillParams {
 
 namespace prefill {
 
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * kWave;
 constexpr int kRows = 128;                       // activation rows per tile
 constexpr int kWaveRows = 64;                    // weight rows per wavefront
-constexpr int kWeightRows = kWaves * kWaveRows;  // 512 weight rows per slice
 constexpr int kChunks = 8;                       // 16-byte chunks per 128-byte stage row
 constexpr int kActChunks = kRows * kChunks;
-constexpr int kWeightChunks = kWeightRows * kChunks;
-constexpr int kActLoads = kActChunks / kWave / kWaves;        // DMA instructions per wave: 2
 constexpr int kWeightLoads = kWaveRows * kChunks / kWave;     // 8 (the wave's own rows)
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-/// bf16: 4 MFMA steps of 16 bytes per stage.
+/// bf16: 4 MFMA steps of 16 bytes per stage; eight wavefronts over 512 weight rows, two 80 KB
+/// LDS stages (measured faster than four wavefronts over 256 rows with three 48 KB stages).
 struct Bf16 {
   static constexpr int kSteps = 4;
   static constexpr int kPieces = 1;  // 16-byte pieces per lane per step
   static constexpr bool kScaled = false;
+  static constexpr int kWaves = 8;
+  static constexpr int kStages = 2;
 };
 
-/// e4m3: 2 MFMA steps of 32 bytes per stage.
+/// e4m3: 2 MFMA steps of 32 bytes per stage; eight wavefronts (two per SIMD: one wave's MFMAs
+/// cover the other's scaling) over 512 weight rows, two 80 KB LDS stages.
 struct E4m3 {
   static constexpr int kSteps = 2;
   static constexpr int kPieces = 2;
   static constexpr bool kScaled = true;
+  static constexpr int kWaves = 8;
+  static constexpr int kStages = 2;
 };
 
-/// Output columns one workgroup covers.
-template <bool kGated>
+/// Weight rows of a slice, and the output columns one workgroup covers.
+template <class F>
+constexpr int weight_rows() {
+  return F::kWaves * kWaveRows;
+}
+template <class F, bool kGated>
 constexpr int slice_width() {
-  return kGated ? kWeightRows / 2 : kWeightRows;
+  return kGated ? weight_rows<F>() / 2 : weight_rows<F>();
 }
 
 __device__ __forceinline__ int key(int row) { return (row >> 1) & 7; }
@@ -116,9 +121,10 @@ __device__ __forceinline__ floatx16 mma(const Operand<F> &w, const Operand<F> &a
   }
 }
 
+template <class F>
 struct Stage {
   u32x4 act[kActChunks];
-  u32x4 weights[kWeightChunks];
+  u32x4 weights[weight_rows<F>() * kChunks];
 };
 
 /// One 16-byte DMA per lane from `base` + `offset` (base wave-uniform, in SGPRs) into LDS at
@@ -140,19 +146,20 @@ __device__ __forceinline__ void dma16(const void *base, uint32_t offset, uint32_
 /// untouched). The compiler sees the wait, so it knows its own loads issued before are complete.
 __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
 
+
 __device__ __forceinline__ uint32_t lds_address(const void *pointer) {
   typedef const __attribute__((address_space(3))) char *lds_pointer;
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_pointer)pointer));
 }
 
 template <class F, bool kGated>
-__global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParams p) {
   constexpr int NS = F::kSteps;
   constexpr int NP = F::kPieces;
-  // Two stages as two objects, so the compiler sees that a DMA into one never aliases reads of
-  // the other.
-  __shared__ Stage stage0;
-  __shared__ Stage stage1;
+  constexpr int kThreads = F::kWaves * kWave;
+  constexpr int kActLoads = kActChunks / kWave / F::kWaves;  // DMA instructions per wave per stage
+  // The DMA is invisible to the compiler, so one array of stages is as good as separate objects.
+  __shared__ Stage<F> ring[F::kStages];
 
   // ---- the work item ----
   const int b = static_cast<int>(blockIdx.x);
@@ -202,7 +209,7 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
   }
   // This wave's 64 weight rows (LDS rows 64 w ..): FC1 rows 0..31 are up rows, 32..63 the gate
   // rows of the same 32 output columns; FC2 rows are 64 consecutive output columns.
-  const int64_t slice_col = static_cast<int64_t>(slice) * slice_width<kGated>();
+  const int64_t slice_col = static_cast<int64_t>(slice) * slice_width<F, kGated>();
   const int64_t wave_col = slice_col + wave * (kGated ? 32 : 64);
   auto weight_row = [&](int j) -> int64_t {  // first weight row of 32-row block j of this wave
     if constexpr (kGated) return j == 0 ? wave_col : p.out_width + wave_col;
@@ -220,7 +227,7 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
     w_block[j] = p.weights + (expert * p.n_total + (block_live[j] ? weight_row(j) : 0)) * row_bytes;
   const uint32_t w_lane = static_cast<uint32_t>((lane / 8) * row_bytes);
   const uint32_t w_chunk = static_cast<uint32_t>((lane & 7) ^ ((lane >> 4) & 3));
-  auto issue = [&](Stage &st, int k) {
+  auto issue = [&](Stage<F> &st, int k) {
     const int64_t offset = static_cast<int64_t>(k) * 128;
     const uint32_t act_lds = lds_address(st.act + wave * kActLoads * kWave);
     const uint32_t weight_lds = lds_address(st.weights + wave * kWaveRows * kChunks);
@@ -267,7 +274,7 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
     }
   };
 
-  auto compute = [&](const Stage &st, int k, int sb) {
+  auto compute = [&](const Stage<F> &st, int sb) {
     // The wave's weight fragments for the whole stage, then one 32-row activation block at a time.
     Operand<F> wf[2][NS];
 #pragma unroll
@@ -310,31 +317,34 @@ __global__ void __launch_bounds__(kThreads) prefill_kernel(PrefillParams p) {
   // stage k multiplies. Each wave waits for its own loads, then the barrier for every wave, so
   // the stage is complete and the other buffer is free to refill. The DMA of the last stage
   // re-reads it (unconditional issue keeps the waits exact). ----
-  issue(stage0, 0);
+  static_assert(F::kStages == 2, "the K loop runs a two-stage ring");
+  issue(ring[0], 0);
   load_scales(0, 0);
   for (int k = 0; k < stages; k += 2) {
     wait_all_loads();
     __syncthreads();
-    issue(stage1, k + 1);
+    issue(ring[1], k + 1);
     load_scales(1, k + 1);
-    compute(stage0, k, 0);
+    compute(ring[0], 0);
     wait_all_loads();
     __syncthreads();
-    issue(stage0, min(k + 2, stages - 1));
+    issue(ring[0], min(k + 2, stages - 1));
     load_scales(0, min(k + 2, stages - 1));
-    compute(stage1, k + 1, 1);
+    compute(ring[1], 1);
   }
+  // The last refills re-read the final stage; they land before the epilogue reuses the LDS.
+  wait_all_loads();
 
   // ---- epilogue: the output tile goes through LDS so the global stores are whole rows. Lane holds
   // token row 32 mi + lane % 32 and, of block j, weight rows 8 q + 4 h + i in element 4 q + i.
   // LDS rows are padded to kOutStride bytes (8 more than a multiple of 256), so the
   // 32 rows one 8-byte write instruction touches fall on distinct banks. Rows 0..63 live in the
   // first stage buffer, rows 64..127 in the second. ----
-  constexpr int kOutCols = slice_width<kGated>();
+  constexpr int kOutCols = slice_width<F, kGated>();
   constexpr int kOutStride = kOutCols * 2 + 8;
-  static_assert(64 * kOutStride <= static_cast<int>(sizeof(Stage)), "the output tile fits the stage buffers");
+  static_assert(64 * kOutStride <= static_cast<int>(sizeof(Stage<F>)), "the output tile fits the stage buffers");
   auto out_row = [&](int m) -> char * {
-    return (m < 64 ? reinterpret_cast<char *>(&stage0) : reinterpret_cast<char *>(&stage1)) + (m & 63) * kOutStride;
+    return (m < 64 ? reinterpret_cast<char *>(&ring[0]) : reinterpret_cast<char *>(&ring[1])) + (m & 63) * kOutStride;
   };
   __syncthreads();  // every wave is done reading the stage buffers
 #pragma unroll
@@ -413,21 +423,21 @@ template <class F, bool kGated>
 inline bool prefill_fits(int64_t K, int64_t out_width) {
   const int64_t row_bytes = K * (F::kScaled ? 1 : 2);
   if (row_bytes % 256 != 0 || row_bytes == 0) return false;
-  if (kGated) return out_width % prefill::slice_width<kGated>() == 0;
+  if (kGated) return out_width % prefill::slice_width<F, kGated>() == 0;
   return out_width % (F::kScaled ? 128 : 32) == 0;
 }
 
 /// Launches the prefill product over `max_tiles` tiles (tiles past `num_tiles` exit at once).
 template <class F, bool kGated>
 inline void launch_prefill(PrefillParams p, int64_t max_tiles, hipStream_t stream, int group = 16) {
-  p.slices = static_cast<int32_t>(ceil_div<int64_t>(p.out_width, prefill::slice_width<kGated>()));
+  p.slices = static_cast<int32_t>(ceil_div<int64_t>(p.out_width, prefill::slice_width<F, kGated>()));
   p.max_tiles = static_cast<int32_t>(max_tiles);
   p.group = group;
   const int64_t work = max_tiles * p.slices;
   p.per_xcd = static_cast<int32_t>(ceil_div<int64_t>(work, 8));
   const int64_t blocks = static_cast<int64_t>(p.per_xcd) * 8;
   hipLaunchKernelGGL((prefill::prefill_kernel<F, kGated>), dim3(static_cast<uint32_t>(blocks)),
-                     dim3(prefill::kThreads), 0, stream, p);
+                     dim3(F::kWaves * kWave), 0, stream, p);
 }
 
 }  // namespace uniserve
