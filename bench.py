@@ -279,7 +279,11 @@ def traffic_summary(directory):
         write = counter_means(root / name / "write", "WRITE_SIZE")
         entry = {}
         for product, gated in products.items():
-            found = [(k, m) for k, m in ((k, pattern.search(k)) for k in fetch) if m and m.group(2).endswith(gated)]
+            def gated_flag(match):  # stream kernels: <gated[, split]>; prefill kernels: <format, gated>
+                args = [a.strip() for a in match.group(2).split(",")]
+                return args[0] if match.group(1).startswith("stream") else args[-1]
+
+            found = [(k, m) for k, m in ((k, pattern.search(k)) for k in fetch) if m and gated_flag(m) == gated]
             if not found:
                 continue
             kernel, match = found[0]
