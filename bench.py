@@ -113,8 +113,6 @@ def measure(w, steps, warmup):
     """Times `steps` layer calls (after `warmup`), and the FC1 / FC2 kernels inside them."""
     import torch
 
-    from uniserve_moe import ops
-
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         w.step()
@@ -126,22 +124,11 @@ def measure(w, steps, warmup):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
 
-    # The dominant kernels, launched as the layer launches them, timed with events on their stream.
-    maps_view = layer_maps(w)
-    rows = w.layer.views.permuted_rows
-    gated = w.layer.view("gated", torch.bfloat16, (rows, w.intermediate))
-    products = w.layer.view("products", torch.bfloat16, (rows, w.hidden))
+    # The dominant kernels, launched exactly as the layer launches them (its own step entry, same
+    # arguments and workspace), timed with events on their stream.
     fc = {"gather_gemm": [], "route_gemm": []}
-    if w.wdtype == "f8e4m3":
-        xq = w.layer.view("hidden_q", torch.uint8, (w.tokens, w.hidden))
-        xs = w.layer.view("hidden_s", torch.float32, (w.tokens, w.hidden // 128))
-        gq = w.layer.view("gated_q", torch.uint8, (rows, w.intermediate))
-        gs = w.layer.view("gated_s", torch.float32, (rows, w.intermediate // 128))
-        fc1 = lambda: ops.gather_gemm_fp8(xq, xs, w.up_gate, w.scales["up_gate_scales"], w.top, maps_view, rows, out=gated)  # noqa: E731
-        fc2 = lambda: ops.route_gemm_fp8(gq, gs, w.down, w.scales["down_scales"], maps_view, out=products)  # noqa: E731
-    else:
-        fc1 = lambda: ops.gather_gemm(w.x, w.up_gate, w.top, maps_view, rows, out=gated)  # noqa: E731
-        fc2 = lambda: ops.route_gemm(gated, w.down, maps_view, out=products)  # noqa: E731
+    fc1 = lambda: w.layer.step("gather")  # noqa: E731
+    fc2 = lambda: w.layer.step("route")  # noqa: E731
     for _ in range(max(3, warmup // 4)):
         fc1()
         fc2()
@@ -156,26 +143,6 @@ def measure(w, steps, warmup):
     torch.cuda.synchronize()
     kernel_ms = {name: sum(a.elapsed_time(b) for a, b in pairs) / len(pairs) for name, pairs in fc.items()}
     return elapsed, kernel_ms
-
-
-def layer_maps(w):
-    """The layer workspace's sort maps as the [7, rows] view the entry wrappers take."""
-    import torch
-
-    from uniserve_moe import ops
-
-    v = w.layer.views
-    rows = v.permuted_rows
-
-    class Maps:
-        def __getitem__(self, index):
-            name = ["tile_to_expert", "tile_to_limit", "expanded_to_permuted", "permuted_to_expanded",
-                    "permuted_to_token", "total_padded_tokens", "num_non_exiting_tiles"][index]
-            length = {0: v.max_tiles, 1: v.max_tiles, 2: w.tokens * w.top, 3: rows, 4: rows, 5: 1, 6: 1}[index]
-            return w.layer.view(name, torch.int32, (length,))
-
-    del ops
-    return Maps()
 
 
 def algorithmic(w):
@@ -193,7 +160,10 @@ def algorithmic(w):
     layer_bytes = touched * 3 * H * I * elem + scale_bytes + T * H * 2 * 2 + H * E * 2
     layer_flops = 2 * routes * 3 * H * I + 2 * T * H * E
     act_elem = 1 if w.wdtype == "f8e4m3" else 2
-    fc1_bytes = touched * 2 * I * H * elem + T * H * act_elem + routes * I * 2
+    # FC1 writes the gated rows in bf16, or (e4m3 prefill shapes) as e4m3 codes with a scale per
+    # 128 columns.
+    gated_elem = 1 + 4 / 128 if w.wdtype == "f8e4m3" and w.layer.views.route_scales else 2
+    fc1_bytes = touched * 2 * I * H * elem + T * H * act_elem + int(routes * I * gated_elem)
     if w.wdtype == "f8e4m3":
         fc1_bytes += touched * (2 * I // 128) * (H // 128) * 4 + T * (H // 128) * 4
     fc1_flops = 2 * routes * 2 * I * H

@@ -61,7 +61,12 @@ struct uniserve_moe_layer_views {
   int64_t hidden_q;            ///< fp8: [tokens, hidden_size] e4m3
   int64_t hidden_s;            ///< fp8: [tokens, hidden_size / 128] f32
   int64_t gated_q;             ///< fp8: [permuted_rows, intermediate] e4m3
-  int64_t gated_s;             ///< fp8: [permuted_rows, intermediate / 128] f32
+  int64_t gated_s;             ///< fp8: [permuted_rows, intermediate / 128] f32, or with
+                               ///< route_scales [intermediate / 128, permuted_rows]
+  int64_t hidden_route_s;      ///< fp8 with route_scales: [hidden_size / 128, permuted_rows] f32,
+                               ///< the scale of each route's token by permuted row; else -1
+  int64_t route_scales;        ///< 1 when the fp8 products take their activation scales
+                               ///< route-major (prefill shapes), else 0
   int64_t max_tiles;
   int64_t permuted_rows;
   int64_t total;
@@ -73,6 +78,25 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_views_of(int64_t tokens, int64_t hi
                                                       struct uniserve_moe_layer_views *views);
 
 UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_call *call, void *stream);
+
+/// The layer's launches in order; the e4m3 steps launch nothing for bf16 weights, and
+/// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised.
+enum uniserve_moe_layer_step {
+  UNISERVE_MOE_LAYER_ROUTER = 0,
+  UNISERVE_MOE_LAYER_TOPK = 1,
+  UNISERVE_MOE_LAYER_SORT = 2,
+  UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN = 3,
+  UNISERVE_MOE_LAYER_GATHER = 4,
+  UNISERVE_MOE_LAYER_QUANTIZE_GATED = 5,
+  UNISERVE_MOE_LAYER_ROUTE = 6,
+  UNISERVE_MOE_LAYER_UNPERMUTE = 7,
+};
+
+/// One step of `uniserve_moe_layer` alone, exactly as the full call launches it, over the
+/// workspace a full call with the same arguments left (for profiling a step inside the layer;
+/// no counterpart in the reference).
+UNISERVE_EXTERN_C int32_t uniserve_moe_layer_step(const struct uniserve_moe_layer_call *call, int32_t step,
+                                                  void *stream);
 
 /// `ops::moe::max_tiles` (crates/ops/src/moe/mod.rs:63-70): the most tiles `tokens * top` routes
 /// over `local_experts` can fill at `tile` rows per tile.

@@ -243,7 +243,9 @@ def test_prefill_fc1_quantises_like_the_quantiser(device):
     torch.cuda.synchronize()
     rows = layer.views.permuted_rows
     fused_q = layer.view("gated_q", torch.uint8, (rows, intermediate)).cpu().numpy()
-    fused_s = layer.view("gated_s", torch.float32, (rows, intermediate // 128)).cpu().numpy()
+    # Prefill shapes keep both products' activation scales route-major (block by permuted row).
+    assert layer.views.route_scales == 1
+    fused_s = layer.view("gated_s", torch.float32, (intermediate // 128, rows)).cpu().numpy().T
 
     class Maps:
         def __getitem__(self, index):
@@ -264,3 +266,31 @@ def test_prefill_fc1_quantises_like_the_quantiser(device):
     assert live.size == tokens * top
     np.testing.assert_array_equal(fused_q[live], want_q.cpu().numpy()[live])
     np.testing.assert_array_equal(fused_s[live].view(np.uint32), want_s.cpu().numpy()[live].view(np.uint32))
+    # Each route's row of the route-major hidden scales is its token's row of the quantiser's.
+    route_s = layer.view("hidden_route_s", torch.float32, (hidden // 128, rows)).cpu().numpy().T
+    tokens_of = p2e[live] // top
+    np.testing.assert_array_equal(route_s[live].view(np.uint32), xs.cpu().numpy()[tokens_of].view(np.uint32))
+
+
+@pytest.mark.parametrize("wdtype,tokens", [("bf16", 64), ("f8e4m3", 64), ("f8e4m3", 2048)])
+def test_layer_steps_replay_the_call(device, wdtype, tokens):
+    """Every step launched alone over the workspace of a full call, in order, reproduces the call's
+    output bit for bit (the step entry launches what the call launches)."""
+    announce("layer steps", wdtype, tokens)
+    hidden, experts, top, intermediate = 2048, 128, 8, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 50)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+    args = {}
+    if wdtype == "f8e4m3":
+        q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+        up_gate, down = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+        args = dict(up_gate_scales=torch.from_numpy(s1).to(device), down_scales=torch.from_numpy(s2).to(device))
+    out = layer(x, router, up_gate, down, **args)
+    want = bf16_bits(out).copy()
+    out.zero_()
+    layer.view("products", torch.bfloat16, (layer.views.permuted_rows, hidden)).zero_()
+    for name in ops.MoeLayer.STEPS:
+        layer.step(name)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bf16_bits(out), want)

@@ -69,6 +69,8 @@ struct GroupedFp8Params {
   int64_t top;
   uint8_t *out_codes;           ///< FC1 only, or null: the gated rows as e4m3 [permuted_rows, out_width]
   float *out_code_scales;       ///< with out_codes: [permuted_rows, out_width / 128]
+  int64_t scale_rows;           ///< nonzero (prefill kernel only): act_scales and out_code_scales are
+                                ///< route-major, [blocks, scale_rows] by permuted row
 };
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
@@ -77,6 +79,12 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
                         hipStream_t stream);
 bool fp8_stream_path(int64_t routes, int64_t experts);
 
+/// The quantiser over token rows that also scatters each scale to the permuted rows of the
+/// token's routes: route_scales[g, expanded_to_permuted[t, k]] for every held route (k < top).
+void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scales, float *route_scales,
+                                const int32_t *expanded_to_permuted, int64_t top, int64_t route_rows,
+                                int64_t rows, int64_t width, hipStream_t stream);
+
 /// Whether FC1 in e4m3 can write its gated rows already quantised for FC2 (the prefill kernel
 /// serves the shape), which spares the layer the bf16 round trip and the separate quantiser.
 bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate);
@@ -84,6 +92,19 @@ bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hid
 /// The gather_gemm_fp8 entry; with `codes` (and `code_scales`) set, the gated rows are written as
 /// e4m3 codes and per-128-column scales - bit for bit what uniserve_quantize_fp8 makes of the bf16
 /// rows - instead of bf16 (refused unless fp8_fc1_quantizes).
-int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales, void *stream);
+/// With `scale_rows` nonzero, hidden_scales are route-major ([hidden / 128, scale_rows] by permuted
+/// row, as launch_quantize_fp8_routes writes them) and so are the code scales written.
+int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales,
+                        int64_t scale_rows, void *stream);
+
+/// Whether the layer's two e4m3 products both run on the prefill kernel, so both can take
+/// route-major activation scales: one cache line holds 32 consecutive rows' scales of a block,
+/// where row-major scales of gathered token rows cost a line per row.
+bool fp8_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate,
+                      int64_t permuted_rows);
+
+/// The route_gemm_fp8 entry; with `scale_rows` nonzero the row scales are route-major
+/// ([intermediate / 128, scale_rows]; refused unless the prefill kernel serves the shape).
+int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, void *stream);
 
 }  // namespace uniserve

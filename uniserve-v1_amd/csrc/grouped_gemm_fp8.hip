@@ -32,6 +32,10 @@ struct QuantParams {
   int64_t rows;
   int64_t width;
   int32_t input_f32;
+  float *route_scales;                  ///< or null: scales scattered to the routes' permuted rows
+  const int32_t *expanded_to_permuted;  ///< with route_scales: [rows, top]
+  int64_t top;
+  int64_t route_rows;                   ///< with route_scales: its row stride per block
 };
 
 /// 16 lanes per 128-channel group, 8 channels each.
@@ -72,6 +76,12 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
   const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
   *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, scale);
   if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
+  if (p.route_scales != nullptr) {
+    for (int64_t k = sub; k < p.top; k += 16) {
+      const int32_t at = p.expanded_to_permuted[row * p.top + k];
+      if (at >= 0) p.route_scales[column / 128 * p.route_rows + at] = scale;
+    }
+  }
 }
 
 // ---- grouped products --------------------------------------------------------------------------------------
@@ -418,7 +428,16 @@ constexpr int64_t kStreamRowsPerExpert = 24;
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
                          const int32_t *row_limit, int64_t rows, int64_t width, hipStream_t stream) {
-  QuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0};
+  QuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0, nullptr, nullptr, 0, 0};
+  const int64_t groups = rows * (width / 128);
+  const int64_t blocks = ceil_div<int64_t>(groups * 16, kQuantThreads);
+  hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQuantThreads), 0, stream, p);
+}
+
+void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scales, float *route_scales,
+                                const int32_t *expanded_to_permuted, int64_t top, int64_t route_rows,
+                                int64_t rows, int64_t width, hipStream_t stream) {
+  QuantParams p{input, out, scales, nullptr, rows, width, 0, route_scales, expanded_to_permuted, top, route_rows};
   const int64_t groups = rows * (width / 128);
   const int64_t blocks = ceil_div<int64_t>(groups * 16, kQuantThreads);
   hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQuantThreads), 0, stream, p);
@@ -445,6 +464,7 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.top = p.top;
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
+    q.scale_rows = p.scale_rows;
     if (gated) launch_prefill<prefill::E4m3, true>(q, max_tiles, stream);
     else launch_prefill<prefill::E4m3, false>(q, max_tiles, stream);
     return;
@@ -497,7 +517,15 @@ bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hid
   return !fp8_stream_path(tokens * top, experts) && prefill_fits<prefill::E4m3, true>(hidden_size, intermediate);
 }
 
-int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales, void *stream) {
+bool fp8_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate,
+                      int64_t permuted_rows) {
+  const int64_t routes_bound = permuted_rows - (kTileRows - 1) * experts;
+  return fp8_fc1_quantizes(tokens, top, experts, hidden_size, intermediate) &&
+         !fp8_stream_path(routes_bound, experts) && prefill_fits<prefill::E4m3, false>(intermediate, hidden_size);
+}
+
+int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales,
+                        int64_t scale_rows, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_fp8 writes bf16 only");
     if (call->block_n != 128 || call->block_k != 128)
@@ -539,6 +567,11 @@ int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, fl
       p.out_codes = codes;
       p.out_code_scales = code_scales;
     }
+    if (scale_rows != 0) {
+      if (codes == nullptr || scale_rows < call->permuted_rows)
+        return UNISERVE_REFUSE(call, "gather_gemm_fp8 takes route-major scales only as it quantises its output");
+      p.scale_rows = scale_rows;
+    }
     launch_grouped_fp8(p, true, max_tiles, fp8_stream_path(call->tokens * call->top, call->experts),
                        static_cast<hipStream_t>(stream));
     return launched(call, "gather_gemm_fp8");
@@ -548,11 +581,16 @@ int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, fl
 }  // namespace uniserve
 
 extern "C" int32_t uniserve_gather_gemm_fp8(const uniserve_gather_fp8_call *call, void *stream) {
-  return uniserve::gather_gemm_fp8(call, nullptr, nullptr, stream);
+  return uniserve::gather_gemm_fp8(call, nullptr, nullptr, 0, stream);
 }
 
 extern "C" int32_t uniserve_route_gemm_fp8(const uniserve_route_fp8_call *call, void *stream) {
-  using namespace uniserve;
+  return uniserve::route_gemm_fp8(call, 0, stream);
+}
+
+namespace uniserve {
+
+int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "route_gemm_fp8 writes bf16 only");
     if (call->block_n != 128 || call->block_k != 128)
@@ -588,8 +626,15 @@ extern "C" int32_t uniserve_route_gemm_fp8(const uniserve_route_fp8_call *call, 
     p.out_width = call->width;
     p.top = 1;
     const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
-    launch_grouped_fp8(p, false, max_tiles, fp8_stream_path(routes_bound, call->experts),
-                       static_cast<hipStream_t>(stream));
+    const bool stream_path = fp8_stream_path(routes_bound, call->experts);
+    if (scale_rows != 0) {
+      if (stream_path || !prefill_fits<prefill::E4m3, false>(p.K, p.out_width) || scale_rows < call->permuted_rows)
+        return UNISERVE_REFUSE(call, "route_gemm_fp8 takes route-major scales only on the prefill kernel's shapes");
+      p.scale_rows = scale_rows;
+    }
+    launch_grouped_fp8(p, false, max_tiles, stream_path, static_cast<hipStream_t>(stream));
     return launched(call, "route_gemm_fp8");
   });
 }
+
+}  // namespace uniserve

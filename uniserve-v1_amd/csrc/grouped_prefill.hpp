@@ -9,8 +9,10 @@
 //
 //  * Both operands travel HBM/L2 -> LDS by `global_load_lds_dwordx4`: eight lanes cover one
 //    128-byte row, so every load is fully coalesced (rows gathered by the sort's maps for FC1).
-//    Two LDS stages of 80 KB (16 KB activations + 64 KB weights); the loads of stage k + 1 fly
-//    while stage k multiplies, one barrier per stage.
+//    Two LDS stages of 80 KB (16 KB activations + 64 KB weights), one barrier per stage. The
+//    activation rows of stage k + 1 fly while stage k multiplies. bf16 weight rows fly two stages:
+//    a wave reads only its own weight rows, so it refills them with stage k + 2 as soon as it holds
+//    stage k's in registers.
 //  * LDS rows are 8 chunks of 16 bytes, chunk c of row r stored at c ^ key(r) with
 //    key(r) = (r >> 1) & 7: a DMA instruction writes 8 whole rows, and a 16-lane group of an MFMA
 //    fragment read (16 consecutive rows, one logical chunk) hits all 64 banks once - rows of one
@@ -28,9 +30,12 @@
 // Both operands share one permutation of K inside a stage (lane half h holds bytes 64 h .. 64 h + 63
 // of the stage's 128, its steps in order), which changes only the FP32 summation order.
 //
-// Work items (tile, slice) are numbered in groups of `group` consecutive tiles, slice-major inside a
-// group, and handed to the 8 XCDs in contiguous ranges (block b runs on XCD b % 8), so the
-// workgroups resident on one XCD at a time share a few weight slices in that XCD's L2.
+// Work items (tile, slice) come in groups of `group` consecutive tiles, slice-major inside a group;
+// the groups are dealt to the 8 XCDs in turn (block b runs on XCD b % 8; group g on XCD g % 8), and
+// each XCD runs its groups in order. The workgroups resident on one XCD at a time share a few
+// weight slices and activation tiles in that XCD's L2, and every XCD gets a like share of the
+// experts with few tiles, whose weights stream from HBM with no reuse (a contiguous range of tiles
+// per XCD would leave some XCDs all single-tile experts and others one heavy expert).
 #pragma once
 
 #include "common.hpp"
@@ -55,9 +60,11 @@ struct PrefillParams {
   int32_t slices;                ///< weight-row slices per tile
   int32_t max_tiles;
   int32_t group;                 ///< tiles per work group of the numbering
-  int32_t per_xcd;               ///< work items per XCD range
+  int32_t groups_per_xcd;        ///< groups of tiles each XCD runs
   uint8_t *out_codes;            ///< FC1 only, or null: write the gated rows as e4m3 codes
   float *out_code_scales;        ///< with out_codes: [permuted_rows, out_width / 128]
+  int64_t scale_rows;            ///< nonzero: act_scales are [K / 128, scale_rows] and out_code_scales
+                                 ///< [out_width / 128, scale_rows], both indexed by permuted row
 };
 
 namespace prefill {
@@ -142,6 +149,27 @@ __device__ __forceinline__ void dma16(const void *base, uint32_t offset, uint32_
       : "m0");
 }
 
+/// `dma16` preceded by a wait for this wave's outstanding LDS reads, so the DMA cannot overwrite
+/// LDS that an earlier `ds_read` of the wave has not read yet.
+__device__ __forceinline__ void dma16_after_lds_reads(const void *base, uint32_t offset, uint32_t lds) {
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1\n\t"
+      :
+      : "v"(offset), "s"(base), "s"(lds)
+      : "m0");
+}
+
+/// Waits until at most N vector-memory loads of this wave are outstanding (they complete in
+/// issue order); the other counters untouched.
+template <int N>
+__device__ __forceinline__ void wait_loads_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
 /// Waits until every vector-memory load of this wave has landed (vmcnt 0; the other counters
 /// untouched). The compiler sees the wait, so it knows its own loads issued before are complete.
 __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x0f70); }
@@ -163,12 +191,14 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
 
   // ---- the work item ----
   const int b = static_cast<int>(blockIdx.x);
-  const int w_index = (b & 7) * p.per_xcd + (b >> 3);
-  if (w_index >= p.slices * p.max_tiles) return;
-  const int span = p.group * p.slices;
-  const int first_tile = (w_index / span) * p.group;
+  const int span = p.group * p.slices;        // work items of one group of tiles
+  const int seq = b >> 3;                      // this block's place in its XCD's sequence
+  const int group_index = (seq / span) * 8 + (b & 7);
+  const int first_tile = group_index * p.group;
+  if (first_tile >= p.max_tiles) return;
   const int in_group = min(p.group, p.max_tiles - first_tile);
-  const int within = w_index - (w_index / span) * span;
+  const int within = seq - (seq / span) * span;
+  if (within >= in_group * p.slices) return;
   const int slice = within / in_group;
   const int tile = first_tile + within % in_group;
   if (tile >= p.num_tiles[0]) return;
@@ -227,28 +257,43 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
     w_block[j] = p.weights + (expert * p.n_total + (block_live[j] ? weight_row(j) : 0)) * row_bytes;
   const uint32_t w_lane = static_cast<uint32_t>((lane / 8) * row_bytes);
   const uint32_t w_chunk = static_cast<uint32_t>((lane & 7) ^ ((lane >> 4) & 3));
-  auto issue = [&](Stage<F> &st, int k) {
+  auto issue_act = [&](Stage<F> &st, int k) {
     const int64_t offset = static_cast<int64_t>(k) * 128;
     const uint32_t act_lds = lds_address(st.act + wave * kActLoads * kWave);
-    const uint32_t weight_lds = lds_address(st.weights + wave * kWaveRows * kChunks);
 #pragma unroll
     for (int i = 0; i < kActLoads; ++i)
       dma16(p.act + offset, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+  };
+  // `after_reads`: the wave's own weight rows of `st` were just read into registers; the first
+  // DMA waits for those LDS reads (lgkmcnt 0) before it may overwrite them.
+  auto issue_weights = [&](Stage<F> &st, int k, bool after_reads) {
+    const int64_t offset = static_cast<int64_t>(k) * 128;
+    const uint32_t weight_lds = lds_address(st.weights + wave * kWaveRows * kChunks);
 #pragma unroll
-    for (int i = 0; i < kWeightLoads; ++i)
-      dma16(w_block[i / 4] + offset + (i % 4) * 8 * row_bytes, w_lane + ((w_chunk ^ static_cast<uint32_t>(4 * (i & 1))) << 4),
-            __builtin_amdgcn_readfirstlane(weight_lds + i * 8 * kChunks * 16));
+    for (int i = 0; i < kWeightLoads; ++i) {
+      const uint8_t *base = w_block[i / 4] + offset + (i % 4) * 8 * row_bytes;
+      const uint32_t lane_offset = w_lane + ((w_chunk ^ static_cast<uint32_t>(4 * (i & 1))) << 4);
+      const uint32_t lds = __builtin_amdgcn_readfirstlane(weight_lds + i * 8 * kChunks * 16);
+      if (i == 0 && after_reads) dma16_after_lds_reads(base, lane_offset, lds);
+      else dma16(base, lane_offset, lds);
+    }
   };
 
   // ---- e4m3 scales: the activation scales of this lane's four token rows (prefetched a stage
   // ahead) and the weight blocks' scales (wave-uniform) ----
   const int kb_count = static_cast<int>(p.K / 128);
-  int sx_row[4];  // the activation-scale row offset of each of this lane's token rows
+  // The activation scales of this lane's four tile rows: by permuted row, block-major (a stage's
+  // 128 scales are one contiguous run: one cache line per 32 lanes), or row-major by source row
+  // (FC1 gathers them from token rows). Padding rows take the tile's first row.
+  int sx_row[4];
+  const int64_t sx_block_stride = p.scale_rows != 0 ? p.scale_rows : 1;
   const float *sw_src[2];
   if constexpr (F::kScaled) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      sx_row[mi] = static_cast<int>(source_row(mi * 32 + r32)) * kb_count;
+      const int r = mi * 32 + r32;
+      sx_row[mi] = p.scale_rows != 0 ? static_cast<int>(first) + (r < rows ? r : 0)
+                                     : static_cast<int>(source_row(r)) * kb_count;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -268,13 +313,13 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
   auto load_scales = [&](int buffer, int k) {
     if constexpr (F::kScaled) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) sx[buffer][mi] = (p.act_scales + k)[sx_row[mi]];
+      for (int mi = 0; mi < 4; ++mi) sx[buffer][mi] = (p.act_scales + k * sx_block_stride)[sx_row[mi]];
       sw[buffer][0] = sw_src[0][k];
       sw[buffer][1] = sw_src[1][k];
     }
   };
 
-  auto compute = [&](const Stage<F> &st, int sb) {
+  auto compute = [&](const Stage<F> &st, int sb, auto &&after_weight_reads) {
     // The wave's weight fragments for the whole stage, then one 32-row activation block at a time.
     Operand<F> wf[2][NS];
 #pragma unroll
@@ -284,6 +329,7 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
 #pragma unroll
         for (int q = 0; q < NP; ++q)
           wf[j][s].piece[q] = st.weights[slot(wave * kWaveRows + j * 32 + r32, 4 * h + s * NP + q)];
+    after_weight_reads();
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       Operand<F> af[NS];
@@ -313,24 +359,51 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
     }
   };
 
-  // ---- the K loop (an even number of stages): stage k + 1's DMA and activation scales fly while
-  // stage k multiplies. Each wave waits for its own loads, then the barrier for every wave, so
-  // the stage is complete and the other buffer is free to refill. The DMA of the last stage
-  // re-reads it (unconditional issue keeps the waits exact). ----
-  static_assert(F::kStages == 2, "the K loop runs a two-stage ring");
-  issue(ring[0], 0);
-  load_scales(0, 0);
-  for (int k = 0; k < stages; k += 2) {
-    wait_all_loads();
-    __syncthreads();
-    issue(ring[1], k + 1);
-    load_scales(1, k + 1);
-    compute(ring[0], 0);
-    wait_all_loads();
-    __syncthreads();
-    issue(ring[0], min(k + 2, stages - 1));
-    load_scales(0, min(k + 2, stages - 1));
-    compute(ring[1], 1);
+  // ---- the K loop (an even number of stages) ----
+  auto nothing = [] {};
+  if constexpr (F::kScaled) {
+    // e4m3: stage k + 1's DMA and activation scales fly while stage k multiplies. Each wave waits
+    // for its own loads, then the barrier for every wave, so the stage is complete and the other
+    // buffer is free to refill. (The scale loads are compiler-visible: the compiler waits for all
+    // loads before their use, so nothing may stay in flight across a stage here.) The DMA of the
+    // last stage re-reads it (unconditional issue keeps the waits exact).
+    issue_act(ring[0], 0);
+    issue_weights(ring[0], 0, false);
+    load_scales(0, 0);
+    for (int k = 0; k < stages; k += 2) {
+      wait_all_loads();
+      __syncthreads();
+      issue_act(ring[1], k + 1);
+      issue_weights(ring[1], k + 1, false);
+      load_scales(1, k + 1);
+      compute(ring[0], 0, nothing);
+      wait_all_loads();
+      __syncthreads();
+      issue_act(ring[0], min(k + 2, stages - 1));
+      issue_weights(ring[0], min(k + 2, stages - 1), false);
+      load_scales(0, min(k + 2, stages - 1));
+      compute(ring[1], 1, nothing);
+    }
+  } else {
+    // bf16: a wave's weight rows are read by that wave alone, and it holds a stage's weight
+    // fragments in registers before it multiplies. So it refills its own rows of the buffer with
+    // stage k + 2 as soon as it has read stage k's - two stages of cover for 80% of the bytes,
+    // with no barrier in between. The shared activation rows refill after each barrier (stage
+    // k + 1 while k multiplies). At each barrier every load but the wave's latest weight refill
+    // has landed. Loads past the last stage re-read it, keeping the counts exact.
+    issue_act(ring[0], 0);
+    issue_weights(ring[0], 0, false);
+    issue_weights(ring[1], min(1, stages - 1), false);
+    for (int k = 0; k < stages; k += 2) {
+      wait_loads_but<kWeightLoads>();
+      __syncthreads();
+      issue_act(ring[1], k + 1);
+      compute(ring[0], 0, [&] { issue_weights(ring[0], min(k + 2, stages - 1), true); });
+      wait_loads_but<kWeightLoads>();
+      __syncthreads();
+      issue_act(ring[0], min(k + 2, stages - 1));
+      compute(ring[1], 1, [&] { issue_weights(ring[1], min(k + 3, stages - 1), true); });
+    }
   }
   // The last refills re-read the final stage; they land before the epilogue reuses the LDS.
   wait_all_loads();
@@ -398,7 +471,11 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
       const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
       const int64_t column = slice_col + group * 128 + sub * 8;
       *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(v, scale);
-      if (sub == 0) p.out_code_scales[(first + m) * groups_per_row + column / 128] = scale;
+      if (sub == 0) {
+        const int64_t at = p.scale_rows != 0 ? column / 128 * p.scale_rows + first + m
+                                             : (first + m) * groups_per_row + column / 128;
+        p.out_code_scales[at] = scale;
+      }
     }
     return;
   }
@@ -433,9 +510,8 @@ inline void launch_prefill(PrefillParams p, int64_t max_tiles, hipStream_t strea
   p.slices = static_cast<int32_t>(ceil_div<int64_t>(p.out_width, prefill::slice_width<F, kGated>()));
   p.max_tiles = static_cast<int32_t>(max_tiles);
   p.group = group;
-  const int64_t work = max_tiles * p.slices;
-  p.per_xcd = static_cast<int32_t>(ceil_div<int64_t>(work, 8));
-  const int64_t blocks = static_cast<int64_t>(p.per_xcd) * 8;
+  p.groups_per_xcd = static_cast<int32_t>(ceil_div<int64_t>(ceil_div<int64_t>(max_tiles, group), 8));
+  const int64_t blocks = static_cast<int64_t>(p.groups_per_xcd) * group * p.slices * 8;
   hipLaunchKernelGGL((prefill::prefill_kernel<F, kGated>), dim3(static_cast<uint32_t>(blocks)),
                      dim3(F::kWaves * kWave), 0, stream, p);
 }

@@ -56,8 +56,10 @@ bool views_of(int64_t tokens, int64_t hidden, int64_t experts, int64_t top, int6
     v->hidden_s = take(tokens * (hidden / 128) * 4);
     v->gated_q = take(v->permuted_rows * intermediate);
     v->gated_s = take(v->permuted_rows * (intermediate / 128) * 4);
+    v->route_scales = uniserve::fp8_route_scales(tokens, top, experts, hidden, intermediate, v->permuted_rows) ? 1 : 0;
+    v->hidden_route_s = v->route_scales ? take(v->permuted_rows * (hidden / 128) * 4) : -1;
   } else {
-    v->hidden_q = v->hidden_s = v->gated_q = v->gated_s = -1;
+    v->hidden_q = v->hidden_s = v->gated_q = v->gated_s = v->hidden_route_s = -1;
   }
   v->total = at;
   return true;
@@ -90,8 +92,12 @@ extern "C" int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_s
   return v.total;
 }
 
-extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void *stream) {
+namespace {
+
+/// The layer's launches, all of them (`only` < 0) or the one step `only`.
+int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *stream) {
   using namespace uniserve;
+  auto want = [&](int32_t step) { return only < 0 || only == step; };
   return guarded(call, [&]() -> int32_t {
     if (call->hidden == nullptr || call->router == nullptr || call->up_gate == nullptr ||
         call->down == nullptr || call->out == nullptr || call->workspace == nullptr)
@@ -128,12 +134,14 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
     RouterParams rp{static_cast<const uint16_t *>(call->hidden), static_cast<const uint16_t *>(call->router),
                     static_cast<uint16_t *>(at(v.scores)), call->router_bias, call->tokens, call->experts,
                     call->hidden_size, call->hidden_size, call->hidden_size, call->experts, 1.0f};
-    launch_router(rp, s);
-    if (int32_t status = launched(call, "router gemm")) return status;
+    if (want(UNISERVE_MOE_LAYER_ROUTER)) {
+      launch_router(rp, s);
+      if (int32_t status = launched(call, "router gemm")) return status;
+    }
 
     // 2. topk_softmax over the bf16 scores.
     char message[512] = {0};
-    if (uniserve_topk_softmax_launch(at(v.scores), 1, call->experts, static_cast<int32_t>(call->tokens),
+    if (want(UNISERVE_MOE_LAYER_TOPK) && uniserve_topk_softmax_launch(at(v.scores), 1, call->experts, static_cast<int32_t>(call->tokens),
                                      static_cast<int32_t>(call->experts), static_cast<int32_t>(call->top),
                                      call->renormalize ? 1 : 0, nullptr, -1, ids, weights, nullptr,
                                      reinterpret_cast<const uint32_t *>(call->live_tokens), nullptr, stream,
@@ -159,7 +167,7 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
     sort.scales_dtype = UNISERVE_DTYPE_F32;
     sort.live_tokens = call->live_tokens;
     sort.permuted_to_token = p2t;
-    if (uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
+    if (want(UNISERVE_MOE_LAYER_SORT) && uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
 
     // 4-5. The two products.
     if (!fp8) {
@@ -179,7 +187,7 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       fc1.top = call->top;
       fc1.dtype = UNISERVE_DTYPE_BF16;
       fc1.multiprocessors = call->multiprocessors;
-      if (uniserve_gather_gemm(&fc1, stream) != 0) return forward_error(call, "gather_gemm", fc1);
+      if (want(UNISERVE_MOE_LAYER_GATHER) && uniserve_gather_gemm(&fc1, stream) != 0) return forward_error(call, "gather_gemm", fc1);
 
       uniserve_route_call fc2{};
       fc2.rows = at(v.gated);
@@ -195,8 +203,11 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       fc2.experts = call->experts;
       fc2.dtype = UNISERVE_DTYPE_BF16;
       fc2.multiprocessors = call->multiprocessors;
-      if (uniserve_route_gemm(&fc2, stream) != 0) return forward_error(call, "route_gemm", fc2);
+      if (want(UNISERVE_MOE_LAYER_ROUTE) && uniserve_route_gemm(&fc2, stream) != 0) return forward_error(call, "route_gemm", fc2);
     } else {
+      // Prefill shapes: the scales of both products' activations go route-major (block by
+      // permuted row), so a tile's scales of one K block are contiguous.
+      const int64_t scale_rows = v.route_scales ? v.permuted_rows : 0;
       uniserve_quantize_fp8_call qx{};
       qx.input = call->hidden;
       qx.out = at(v.hidden_q);
@@ -205,11 +216,19 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       qx.width = call->hidden_size;
       qx.input_dtype = UNISERVE_DTYPE_BF16;
       qx.group = 128;
-      if (uniserve_quantize_fp8(&qx, stream) != 0) return forward_error(call, "quantize_fp8", qx);
+      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN)) {
+      } else if (scale_rows != 0) {
+        launch_quantize_fp8_routes(static_cast<const uint16_t *>(call->hidden), static_cast<uint8_t *>(at(v.hidden_q)),
+                                   static_cast<float *>(at(v.hidden_s)), static_cast<float *>(at(v.hidden_route_s)), e2p,
+                                   call->top, scale_rows, call->tokens, call->hidden_size, s);
+        if (int32_t status = launched(call, "quantize_fp8")) return status;
+      } else if (uniserve_quantize_fp8(&qx, stream) != 0) {
+        return forward_error(call, "quantize_fp8", qx);
+      }
 
       uniserve_gather_fp8_call fc1{};
       fc1.hidden = at(v.hidden_q);
-      fc1.hidden_scales = static_cast<const float *>(at(v.hidden_s));
+      fc1.hidden_scales = static_cast<const float *>(at(scale_rows != 0 ? v.hidden_route_s : v.hidden_s));
       fc1.weights = call->up_gate;
       fc1.weight_scales = call->up_gate_scales;
       fc1.out = at(v.gated);
@@ -228,9 +247,11 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       fc1.out_dtype = UNISERVE_DTYPE_BF16;
       fc1.multiprocessors = call->multiprocessors;
       const bool fused = fp8_fc1_quantizes(call->tokens, call->top, call->experts, call->hidden_size, call->intermediate);
-      if (fused) {
+      if (!want(UNISERVE_MOE_LAYER_GATHER)) {
+      } else if (fused) {
         // Prefill shapes: FC1 writes the gated rows straight in FC2's e4m3 form.
-        if (gather_gemm_fp8(&fc1, static_cast<uint8_t *>(at(v.gated_q)), static_cast<float *>(at(v.gated_s)), stream) != 0)
+        if (gather_gemm_fp8(&fc1, static_cast<uint8_t *>(at(v.gated_q)), static_cast<float *>(at(v.gated_s)), scale_rows,
+                            stream) != 0)
           return forward_error(call, "gather_gemm_fp8", fc1);
       } else if (uniserve_gather_gemm_fp8(&fc1, stream) != 0) {
         return forward_error(call, "gather_gemm_fp8", fc1);
@@ -245,7 +266,7 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       qg.width = call->intermediate;
       qg.input_dtype = UNISERVE_DTYPE_BF16;
       qg.group = 128;
-      if (!fused && uniserve_quantize_fp8(&qg, stream) != 0) return forward_error(call, "quantize_fp8", qg);
+      if (want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) && !fused && uniserve_quantize_fp8(&qg, stream) != 0) return forward_error(call, "quantize_fp8", qg);
 
       uniserve_route_fp8_call fc2{};
       fc2.rows = at(v.gated_q);
@@ -265,7 +286,7 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
       fc2.block_k = 128;
       fc2.out_dtype = UNISERVE_DTYPE_BF16;
       fc2.multiprocessors = call->multiprocessors;
-      if (uniserve_route_gemm_fp8(&fc2, stream) != 0) return forward_error(call, "route_gemm_fp8", fc2);
+      if (want(UNISERVE_MOE_LAYER_ROUTE) && route_gemm_fp8(&fc2, scale_rows, stream) != 0) return forward_error(call, "route_gemm_fp8", fc2);
     }
 
     // 6. The weighted combine, permuted layout.
@@ -282,7 +303,19 @@ extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void 
     combine.scales_dtype = UNISERVE_DTYPE_F32;
     combine.output_dtype = UNISERVE_DTYPE_BF16;
     combine.layout = UNISERVE_UNPERMUTE_LAYOUT_PERMUTED;
-    if (uniserve_moe_unpermute(&combine, stream) != 0) return forward_error(call, "moe_unpermute", combine);
+    if (want(UNISERVE_MOE_LAYER_UNPERMUTE) && uniserve_moe_unpermute(&combine, stream) != 0) return forward_error(call, "moe_unpermute", combine);
     return 0;
   });
+}
+
+}  // namespace
+
+extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void *stream) {
+  return run_layer(call, -1, stream);
+}
+
+extern "C" int32_t uniserve_moe_layer_step(const uniserve_moe_layer_call *call, int32_t step, void *stream) {
+  if (step < UNISERVE_MOE_LAYER_ROUTER || step > UNISERVE_MOE_LAYER_UNPERMUTE)
+    return ::uniserve::refuse_into(const_cast<char *>(call->error), "moe_layer_step: no step %d", step);
+  return run_layer(call, step, stream);
 }

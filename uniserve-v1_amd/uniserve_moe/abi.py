@@ -257,6 +257,8 @@ class LayerViews(ctypes.Structure):
             "hidden_s",
             "gated_q",
             "gated_s",
+            "hidden_route_s",
+            "route_scales",
             "max_tiles",
             "permuted_rows",
             "total",
@@ -323,6 +325,8 @@ def library():
     for name in ("uniserve_moe_layer_workspace",):
         getattr(lib, name).argtypes = [_I64] * 6
         getattr(lib, name).restype = _I64
+    lib.uniserve_moe_layer_step.argtypes = [ctypes.POINTER(LayerCall), ctypes.c_int32, _P]
+    lib.uniserve_moe_layer_step.restype = ctypes.c_int32
     lib.uniserve_moe_layer_views_of.argtypes = [_I64] * 6 + [ctypes.POINTER(LayerViews)]
     lib.uniserve_moe_layer_views_of.restype = ctypes.c_int32
     lib.uniserve_moe_max_tiles.argtypes = [_I64] * 4

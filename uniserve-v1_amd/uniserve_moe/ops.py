@@ -285,3 +285,13 @@ class MoeLayer:
         call.multiprocessors = multiprocessors(hidden.device)
         _check(library().uniserve_moe_layer(ctypes.byref(call), _stream(hidden.device)), call, "moe_layer")
         return out
+
+    STEPS = ("router", "topk", "sort", "quantize_hidden", "gather", "quantize_gated", "route", "unpermute")
+
+    def step(self, name):
+        """Launches one step of the last call again, exactly as the call launched it (same
+        arguments, same workspace)."""
+        index = self.STEPS.index(name)
+        device = self.workspace.device
+        _check(library().uniserve_moe_layer_step(ctypes.byref(self.call), index, _stream(device)), self.call,
+               "moe_layer_step")
