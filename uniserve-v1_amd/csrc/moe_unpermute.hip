@@ -56,16 +56,34 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
   float sum[kPerLane];
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) sum[j] = 0.0f;
-  for (int64_t k = 0; k < p.top; ++k) {
-    const int64_t slot = token * p.top + k;
-    const int32_t entry = p.expanded_to_permuted[slot];
-    if (entry < 0 || entry >= p.routes_rows) continue;
-    const int64_t row = p.expanded ? slot : entry;
-    const float weight = widen<Scale>(scales[slot]);
-    const uint4 packed = *reinterpret_cast<const uint4 *>(routes + row * p.hidden + column);
-    const Element *values = reinterpret_cast<const Element *>(&packed);
+  // Routes in batches of kBatch: the batch's map entries and weights, then its route rows, are
+  // loaded before any is used (two round trips per batch, not two per route); the sum still
+  // takes the routes in order.
+  constexpr int kBatch = 8;
+  for (int64_t k0 = 0; k0 < p.top; k0 += kBatch) {
+    int32_t entry[kBatch];
+    float weight[kBatch];
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j) sum[j] = __builtin_fmaf(weight, widen<Element>(values[j]), sum[j]);
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t slot = token * p.top + k0 + u;
+      const bool exists = k0 + u < p.top;
+      entry[u] = exists ? p.expanded_to_permuted[slot] : -1;
+      weight[u] = exists ? widen<Scale>(scales[slot]) : 0.0f;
+    }
+    uint4 packed[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const bool visible = entry[u] >= 0 && entry[u] < p.routes_rows;
+      const int64_t row = p.expanded ? token * p.top + k0 + u : entry[u];
+      packed[u] = visible ? *reinterpret_cast<const uint4 *>(routes + row * p.hidden + column) : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (entry[u] < 0 || entry[u] >= p.routes_rows) continue;
+      const Element *values = reinterpret_cast<const Element *>(&packed[u]);
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j) sum[j] = __builtin_fmaf(weight[u], widen<Element>(values[j]), sum[j]);
+    }
   }
   Element result[kPerLane];
 #pragma unroll

@@ -8,7 +8,7 @@
 // Two kernels. Batches large enough to fill the chip with 64 x 64 output tiles take 64-deep K
 // steps through two XOR-swizzled LDS buffers, their loads eight steps ahead in registers. Smaller ones (decode: 64 tokens x 128 experts is two such
 // tiles) use 16 x 16 tiles whose contraction is split over the eight wavefronts of a workgroup:
-// each wave loads its K steps straight into registers, four steps in flight, and the partial
+// each wave loads its K steps straight into registers, eight steps in flight, and the partial
 // sums meet in LDS in wave order. In both, weight rows are MFMA operand A and token rows
 // operand B, so each lane holds four consecutive expert scores of one token.
 #include "common.hpp"
@@ -109,7 +109,7 @@ __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) 
 }
 
 constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyUnroll = 4;
+constexpr int kSkinnyUnroll = 8;  // a hidden size of 2048 is one batch of loads per wavefront
 
 __global__ void __launch_bounds__(kSkinnyWaves * kWave) skinny_router_kernel(RouterParams p) {
   __shared__ floatx4 partial[kSkinnyWaves][kWave];

@@ -7,8 +7,8 @@
 // rounding depends on their order, and the selection compares them for equality, so the routine
 // keeps the reference's reduction tree exactly (crates/ops/kernels/topk_softmax/nvcc/src/
 // topk_softmax.cu:106-199): lane j of a half holds experts j + 32 i, sums its own terms in i
-// order, and the halves exchange by xor butterflies over 16, 8, 4, 2, 1 within the half (DPP quad
-// permutes for 1 and 2, ds_swizzle bit-mask mode for 4, 8 and 16).
+// order, and the halves exchange by xor butterflies over 16, 8, 4, 2, 1 within the half (DPP for
+// 1, 2, 4 and 8, the gfx950 row swap for 16).
 //
 // The exponential is the library's own (`router_expf`) and not the platform's, so that the CPU
 // oracle evaluates the identical operations: every probability, and therefore every id, is
@@ -51,16 +51,28 @@ __device__ __forceinline__ float router_expf(float x) {
   return (p * first) * second;
 }
 
-/// The value of lane (this lane xor kOffset), within each 32-lane half.
+/// The value of lane (this lane xor kOffset), within each 32-lane half: VALU lane exchanges only
+/// (DPP within a 16-lane row, the row swap across rows), no trip through the LDS crossbar.
 template <int kOffset>
 __device__ __forceinline__ int xor_lane(int value) {
   if constexpr (kOffset == 1) {
     return __builtin_amdgcn_mov_dpp(value, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
   } else if constexpr (kOffset == 2) {
     return __builtin_amdgcn_mov_dpp(value, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (kOffset == 4) {
+    // Lanes with bit 2 clear read 4 lanes up (row_shl:4), the others 4 lanes down (row_shr:4);
+    // neither leaves its 16-lane row.
+    const int up = __builtin_amdgcn_mov_dpp(value, 0x104, 0xF, 0xF, false);
+    const int down = __builtin_amdgcn_mov_dpp(value, 0x114, 0xF, 0xF, false);
+    return (lane_id() & 4) ? down : up;
+  } else if constexpr (kOffset == 8) {
+    return __builtin_amdgcn_mov_dpp(value, 0x128, 0xF, 0xF, false);  // row_ror:8 = xor 8 in a row
   } else {
-    // Bit-mask swizzle over 32 lanes: and 0x1f, or 0, xor kOffset.
-    return __builtin_amdgcn_ds_swizzle(value, (kOffset << 10) | 0x1F);
+    static_assert(kOffset == 16, "exchanges within a 32-lane half");
+    // Swapping the odd rows of one copy with the even rows of another leaves, in each lane, its
+    // own row in the first result and its partner row in the second (or the reverse for odd rows).
+    const auto swapped = __builtin_amdgcn_permlane16_swap(value, value, false, false);
+    return (lane_id() & 16) ? static_cast<int>(swapped[0]) : static_cast<int>(swapped[1]);
   }
 }
 
