@@ -62,6 +62,7 @@ class Workload:
         import torch
 
         from uniserve_moe import ops
+        from uniserve_moe.checkpoint import quantize_blocks_e4m3
 
         self.name = name
         (self.tokens, self.hidden, self.experts, self.top, self.intermediate, self.wdtype,
@@ -82,8 +83,9 @@ class Workload:
             self.bias = (-1.1 * torch.log(torch.arange(E, device=device, dtype=torch.float32) + 1.0)).contiguous()
         self.scales = {}
         if self.wdtype == "f8e4m3":
-            self.up_gate, s1 = quantize_blocks(self.up_gate_bf16)
-            self.down, s2 = quantize_blocks(self.down_bf16)
+            # Setup, not timed: 128 x 128 block-scaled e4m3 (scale = blockmax / 448).
+            self.up_gate, s1 = quantize_blocks_e4m3(self.up_gate_bf16)
+            self.down, s2 = quantize_blocks_e4m3(self.down_bf16)
             self.scales = dict(up_gate_scales=s1, down_scales=s2)
         else:
             self.up_gate, self.down = self.up_gate_bf16, self.down_bf16
@@ -93,20 +95,6 @@ class Workload:
     def step(self):
         return self.layer(self.x, self.router, self.up_gate, self.down, out=self.out,
                           router_bias=self.bias, **self.scales)
-
-
-def quantize_blocks(w):
-    """128 x 128 block-scaled e4m3 of a bf16 [E, N, K] stack on the device (setup, not timed):
-    scale = blockmax / 448, codes = e4m3fn(w / scale), torch's round-to-nearest-even cast."""
-    import torch
-
-    E, N, K = w.shape
-    blocks = w.float().reshape(E, N // 128, 128, K // 128, 128)
-    amax = blocks.abs().amax(dim=(2, 4), keepdim=True)
-    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
-    codes = (blocks / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
-    return (codes.reshape(E, N, K).view(torch.uint8).contiguous(),
-            scale.reshape(E, N // 128, K // 128).contiguous())
 
 
 def measure(w, steps, warmup):
