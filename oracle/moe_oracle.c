@@ -537,6 +537,29 @@ void oracle_moe_unpermute(const uint16_t *routes, const int32_t *expanded_to_per
   }
 }
 
+/* sigmoid_gated_add (crates/ops/src/residual.rs:808-811; CPU form crates/nn/src/functional/moe.rs:1589-1600):
+ * target[r, c] = round(target[r, c] + sigmoid(gate[r]) * update[r, c]), FP32 arithmetic, elements of
+ * `kind` (0 f32, 1 bf16, 2 f16) as raw bits. */
+static float widen_kind(const void *data, int32_t kind, int64_t index) {
+  if (kind == 0) return ((const float *)data)[index];
+  if (kind == 2) return oracle_f32_from_f16(((const uint16_t *)data)[index]);
+  return oracle_f32_from_bf16(((const uint16_t *)data)[index]);
+}
+
+void oracle_sigmoid_gated_add(void *target, const void *update, const void *gate, int64_t rows,
+                              int64_t columns, int32_t kind) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float g = 1.0f / (1.0f + expf(-widen_kind(gate, kind, r)));
+    for (int64_t c = 0; c < columns; ++c) {
+      const int64_t i = r * columns + c;
+      const float sum = widen_kind(target, kind, i) + g * widen_kind(update, kind, i);
+      if (kind == 0) ((float *)target)[i] = sum;
+      else if (kind == 2) ((uint16_t *)target)[i] = oracle_f16_from_f32(sum);
+      else ((uint16_t *)target)[i] = oracle_bf16_from_f32(sum);
+    }
+  }
+}
+
 /* ---- block-scaled fp8 (no reference counterpart: parity unpinned against the reference;
  *      crates/nn/src/quantization.rs:241-249 refuses this format) ------------------------------ */
 

@@ -65,6 +65,11 @@ void oracle_moe_unpermute(const uint16_t *routes, const int32_t *expanded_to_per
                           const float *scales, int64_t tokens, int64_t top, int64_t hidden,
                           int64_t routes_rows, int32_t layout, float *out);
 
+/* ---- the shared expert's join ---------------------------------------------------------------- */
+/* kind: 0 f32, 1 bf16, 2 f16 (raw bits); target updated in place. */
+void oracle_sigmoid_gated_add(void *target, const void *update, const void *gate, int64_t rows,
+                              int64_t columns, int32_t kind);
+
 /* ---- block-scaled fp8 ---------------------------------------------------------------------- */
 void oracle_quantize_rows_fp8(const uint16_t *in_bf16, int64_t rows, int64_t width, int64_t group,
                               uint8_t *out, float *scales);

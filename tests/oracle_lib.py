@@ -51,6 +51,7 @@ _sig("oracle_gather_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P
 _sig("oracle_route_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
 _sig("oracle_moe_layer", [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P], _I32)
 _sig("oracle_threads", [], _I32)
+_sig("oracle_sigmoid_gated_add", [_P, _P, _P, _I64, _I64, _I32])
 
 KINDS = {np.dtype(np.float32): 0, "bf16": 1, np.dtype(np.float16): 2}
 
@@ -103,6 +104,17 @@ def sequence(count, seed):
 def normal(count, seed, stddev=1.0, mean=0.0):
     out = np.empty(count, dtype=np.float32)
     LIB.oracle_normal(count, seed, mean, stddev, _p(out))
+    return out
+
+
+def sigmoid_gated_add(target, update, gate, kind):
+    """In place on a copy: ``target`` [rows, columns] += sigmoid(gate[rows]) * update; kind 0 f32
+    (float32 arrays), 1 bf16 / 2 f16 (uint16 bits). Returns the new target."""
+    out = np.array(target, copy=True, order="C")
+    update = np.ascontiguousarray(update)
+    gate = np.ascontiguousarray(gate)
+    rows, columns = out.shape
+    LIB.oracle_sigmoid_gated_add(_p(out), _p(update), _p(gate), rows, columns, kind)
     return out
 
 

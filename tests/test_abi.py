@@ -80,6 +80,9 @@ def test_the_library_exports_every_declared_entry():
     # The router kernel, by the name the reference's operator launches.
     assert hasattr(lib, "uniserve_topk_softmax")
     assert b"uniserve_topk_softmax" in abi.code_object_path().read_bytes()
+    for kernel in (b"uniserve_sigmoid_gated_add_bf16", b"uniserve_sigmoid_gated_add_f16", b"uniserve_sigmoid_gated_add_f32"):
+        assert hasattr(lib, kernel.decode())
+        assert kernel in abi.residual_code_object_path().read_bytes()
 
 
 def message(call):
@@ -173,3 +176,18 @@ def test_layer_workspace_and_refusals():
     assert lib.uniserve_moe_layer_workspace(64, 2048, 128, 8, 768, abi.DTYPE["f16"]) == -1
     call = abi.LayerCall()
     assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "needs hidden" in message(call)
+
+
+def test_sigmoid_gated_add_refusals():
+    """The operator's refusals (crates/ops/src/residual.rs:820-853), before any launch."""
+    lib = abi.library()
+    error = ctypes.create_string_buffer(512)
+    p = ctypes.c_void_p(16)
+    assert lib.uniserve_sigmoid_gated_add_launch(p, p, p, 4, 0, abi.DTYPE["bf16"], None, error, 512) != 0
+    assert b"zero elements" in error.value
+    assert lib.uniserve_sigmoid_gated_add_launch(p, p, p, 1 << 20, 1 << 12, abi.DTYPE["bf16"], None, error, 512) != 0
+    assert b"32-bit" in error.value
+    assert lib.uniserve_sigmoid_gated_add_launch(None, p, p, 4, 8, abi.DTYPE["bf16"], None, error, 512) != 0
+    assert lib.uniserve_sigmoid_gated_add_launch(p, p, p, 4, 8, abi.DTYPE["f8e4m3"], None, error, 512) != 0
+    assert b"bf16, f16 or f32" in error.value
+    assert lib.uniserve_sigmoid_gated_add_launch(None, None, None, 0, 8, abi.DTYPE["bf16"], None, error, 512) == 0

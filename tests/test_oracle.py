@@ -529,3 +529,48 @@ def test_sequence_is_the_reference_lcg_shape():
     assert s.min() >= -1.0 and s.max() < 1.0
     assert np.all(np.round((s + 1.0) * 2**23) == (s + 1.0) * 2**23)
     assert not np.array_equal(s, O.sequence(1000, 1))
+
+
+# ---- the shared expert's join ---------------------------------------------------------------------
+
+
+def test_sigmoid_gated_add_reference_case():
+    """crates/nn/tests/moe.rs:1865-1886: 3 x 4 rows from sequence(.., 90) and sequence(.., 91), gates
+    [0.5, -1.5, 2.0], against the closed form target + update / (1 + e^-gate) (float64 here)."""
+    rows, width = 3, 4
+    target = O.sequence(rows * width, 90).reshape(rows, width)
+    update = O.sequence(rows * width, 91).reshape(rows, width)
+    gate = np.array([0.5, -1.5, 2.0], dtype=np.float32)
+    got = O.sigmoid_gated_add(target, update, gate, 0)
+    want = target.astype(np.float64) + update.astype(np.float64) / (1.0 + np.exp(-gate.astype(np.float64)))[:, None]
+    # One sigmoid (a few ulps), one product and one sum, in FP32.
+    np.testing.assert_allclose(got, want, rtol=0, atol=8 * np.finfo(np.float32).eps * np.abs(want).max())
+    # A zero update leaves the target exactly; a gate of -inf adds nothing, +inf adds the update.
+    np.testing.assert_array_equal(O.sigmoid_gated_add(target, np.zeros_like(update), gate, 0), target)
+    inf_gate = np.array([-np.inf, np.inf, 0.0], dtype=np.float32)
+    got = O.sigmoid_gated_add(target, update, inf_gate, 0)
+    np.testing.assert_array_equal(got[0], target[0])
+    np.testing.assert_array_equal(got[1], target[1] + update[1])
+    np.testing.assert_array_equal(got[2], target[2] + np.float32(0.5) * update[2])
+
+
+def test_sigmoid_gated_add_rounds_once_into_bf16_and_f16():
+    """The narrow types: the FP32 sum of the widened operands, rounded once (bf16 bits, f16 bits)."""
+    rng = np.random.default_rng(3)
+    t = rng.normal(size=(5, 24)).astype(np.float32)
+    u = rng.normal(size=(5, 24)).astype(np.float32)
+    g = rng.normal(size=5).astype(np.float32)
+    tb, ub, gb = O.bf16_encode(t), O.bf16_encode(u), O.bf16_encode(g)
+    got = O.sigmoid_gated_add(tb, ub, gb, 1)
+    gd = O.bf16_decode(gb).astype(np.float32)
+    s = (np.float32(1) / (np.float32(1) + np.exp(-gd).astype(np.float32))).astype(np.float32)
+    want = O.bf16_encode(O.bf16_decode(tb) + s[:, None] * O.bf16_decode(ub))
+    # One FP32 product and sum differ from numpy's float32 evaluation by at most one bf16 step at a
+    # rounding boundary; equal almost everywhere.
+    assert np.mean(got == want) > 0.97
+    assert np.abs(got.astype(np.int32) - want.astype(np.int32)).max() <= 1
+    th, uh, gh = t.astype(np.float16), u.astype(np.float16), g.astype(np.float16)
+    got_h = O.sigmoid_gated_add(th.view(np.uint16), uh.view(np.uint16), gh.view(np.uint16), 2).view(np.float16)
+    sh = 1.0 / (1.0 + np.exp(-gh.astype(np.float64)))
+    want_h = (th.astype(np.float64) + sh[:, None] * uh.astype(np.float64)).astype(np.float16)
+    assert np.abs(got_h.astype(np.float64) - want_h.astype(np.float64)).max() <= np.abs(want_h).max() * 2.0 ** -10

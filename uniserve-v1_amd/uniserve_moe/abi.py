@@ -287,6 +287,11 @@ def code_object_path():
     return _PACKAGE / "uniserve_topk_softmax.hsaco"
 
 
+def residual_code_object_path():
+    """The shared-expert join's code object (``uniserve_sigmoid_gated_add_{bf16,f16,f32}``)."""
+    return _PACKAGE / "uniserve_residual.hsaco"
+
+
 _LIBRARY = None
 
 _ENTRIES = {
@@ -325,6 +330,9 @@ def library():
     for name in ("uniserve_moe_layer_workspace",):
         getattr(lib, name).argtypes = [_I64] * 6
         getattr(lib, name).restype = _I64
+    lib.uniserve_sigmoid_gated_add_launch.argtypes = [_P, _P, _P, _I64, _I64, ctypes.c_int32, _P, ctypes.c_char_p,
+                                                      ctypes.c_size_t]
+    lib.uniserve_sigmoid_gated_add_launch.restype = ctypes.c_int32
     lib.uniserve_moe_layer_step.argtypes = [ctypes.POINTER(LayerCall), ctypes.c_int32, _P]
     lib.uniserve_moe_layer_step.restype = ctypes.c_int32
     lib.uniserve_moe_layer_views_of.argtypes = [_I64] * 6 + [ctypes.POINTER(LayerViews)]

@@ -73,6 +73,27 @@ def topk_softmax(scores, top, renormalize=True, scale=None, mapping=None, live=N
     return ids, weights
 
 
+_ELEMENT = {torch.bfloat16: DTYPE["bf16"], torch.float16: DTYPE["f16"], torch.float32: DTYPE["f32"]}
+
+
+def sigmoid_gated_add_(target, update, gate):
+    """``functional::sigmoid_gated_add_`` (crates/nn/src/functional/moe.rs:1527-1570): ``target``
+    ``[rows, columns]`` += sigmoid(``gate`` ``[rows, 1]``) * ``update``, in place; returns ``target``."""
+    if target.dim() != 2 or update.shape != target.shape or update.dtype != target.dtype:
+        raise ValueError("sigmoid_gated_add_: the update is the target's shape and element type")
+    if tuple(gate.shape) != (target.shape[0], 1) or gate.dtype != target.dtype:
+        raise ValueError("sigmoid_gated_add_: the gate is one logit per row, of the target's type")
+    if not (target.is_contiguous() and update.is_contiguous() and gate.is_contiguous()):
+        raise ValueError("sigmoid_gated_add_: a strided view has no rows to update in place")
+    error = ctypes.create_string_buffer(512)
+    status = library().uniserve_sigmoid_gated_add_launch(
+        _ptr(target), _ptr(update), _ptr(gate), target.shape[0], target.shape[1], _ELEMENT[target.dtype],
+        _stream(target.device), error, 512)
+    if status != 0:
+        raise RuntimeError(f"sigmoid_gated_add refused the call: {error.value.decode()}")
+    return target
+
+
 def empty_maps(tokens, top, local_experts, device, fill=-7):
     rows = max_tiles(tokens, top, local_experts, TILE) * TILE
     return torch.full((SORT_MAPS, max(rows, tokens * top, 1)), fill, dtype=torch.int32, device=device)
