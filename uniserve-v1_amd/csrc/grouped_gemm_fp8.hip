@@ -38,17 +38,20 @@ struct QuantParams {
   int64_t route_rows;                   ///< with route_scales: its row stride per block
 };
 
-/// 16 lanes per 128-channel group, 8 channels each.
+/// 16 lanes per 128-channel group, 8 channels each; the grid strides over the groups, stopping at
+/// the device-side row limit (the padded rows of a decode batch are a small part of the
+/// worst-case rows the host sizes for).
 __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) {
   const int64_t groups_per_row = p.width / 128;
-  const int64_t group = (static_cast<int64_t>(blockIdx.x) * kQuantThreads + threadIdx.x) / 16;
   const int sub = static_cast<int>(threadIdx.x) & 15;
-  const int64_t row = group / groups_per_row;
   const int64_t limit = p.row_limit != nullptr ? p.row_limit[0] : p.rows;
-  const bool active = row < p.rows && row < limit;
-  const int64_t column = (group % groups_per_row) * 128 + sub * 8;
-  float v[8];
-  if (active) {
+  const int64_t last = (limit < p.rows ? limit : p.rows) * groups_per_row;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kQuantThreads / 16;
+  for (int64_t group = (static_cast<int64_t>(blockIdx.x) * kQuantThreads + threadIdx.x) / 16; group < last;
+       group += stride) {
+    const int64_t row = group / groups_per_row;
+    const int64_t column = (group % groups_per_row) * 128 + sub * 8;
+    float v[8];
     if (p.input_f32) {
       const float *src = static_cast<const float *>(p.input) + row * p.width + column;
       const float4 lo = *reinterpret_cast<const float4 *>(src);
@@ -63,23 +66,19 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
         v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
       }
     }
-  } else {
+    float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-  }
-  float amax = 0.0f;
+    for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
 #pragma unroll
-  for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
-#pragma unroll
-  for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
-  if (!active) return;
-  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-  *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, scale);
-  if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
-  if (p.route_scales != nullptr) {
-    for (int64_t k = sub; k < p.top; k += 16) {
-      const int32_t at = p.expanded_to_permuted[row * p.top + k];
-      if (at >= 0) p.route_scales[column / 128 * p.route_rows + at] = scale;
+    for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+    const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+    *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, scale);
+    if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
+    if (p.route_scales != nullptr) {
+      for (int64_t k = sub; k < p.top; k += 16) {
+        const int32_t at = p.expanded_to_permuted[row * p.top + k];
+        if (at >= 0) p.route_scales[column / 128 * p.route_rows + at] = scale;
+      }
     }
   }
 }
@@ -426,21 +425,24 @@ constexpr int64_t kStreamRowsPerExpert = 24;
 
 }  // namespace
 
+/// Workgroups for `rows` x `width`: one 16-lane group per 128 channels, at most 2048 workgroups
+/// (the kernel strides over the rest).
+uint32_t quantize_blocks(int64_t rows, int64_t width) {
+  const int64_t blocks = ceil_div<int64_t>(rows * (width / 128) * 16, kQuantThreads);
+  return static_cast<uint32_t>(blocks < 2048 ? (blocks > 0 ? blocks : 1) : 2048);
+}
+
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
                          const int32_t *row_limit, int64_t rows, int64_t width, hipStream_t stream) {
   QuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0, nullptr, nullptr, 0, 0};
-  const int64_t groups = rows * (width / 128);
-  const int64_t blocks = ceil_div<int64_t>(groups * 16, kQuantThreads);
-  hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQuantThreads), 0, stream, p);
+  hipLaunchKernelGGL(quantize_kernel, dim3(quantize_blocks(rows, width)), dim3(kQuantThreads), 0, stream, p);
 }
 
 void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scales, float *route_scales,
                                 const int32_t *expanded_to_permuted, int64_t top, int64_t route_rows,
                                 int64_t rows, int64_t width, hipStream_t stream) {
   QuantParams p{input, out, scales, nullptr, rows, width, 0, route_scales, expanded_to_permuted, top, route_rows};
-  const int64_t groups = rows * (width / 128);
-  const int64_t blocks = ceil_div<int64_t>(groups * 16, kQuantThreads);
-  hipLaunchKernelGGL(quantize_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQuantThreads), 0, stream, p);
+  hipLaunchKernelGGL(quantize_kernel, dim3(quantize_blocks(rows, width)), dim3(kQuantThreads), 0, stream, p);
 }
 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
