@@ -685,6 +685,157 @@ void oracle_route_gemm_fp8(const uint8_t *rows, const float *row_scales, const u
   }
 }
 
+/* ---- OCP MX: MXFP4 weights x MXFP8 activations (no reference counterpart: the reference's
+ *      four-bit experts are NVFP4, crates/ops/src/moe/grouped.rs:579-1772; parity unpinned
+ *      against the reference) --------------------------------------------------------------- */
+
+/* E2M1: sign, two exponent bits (bias 1), one mantissa bit: magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6. */
+float oracle_f32_from_e2m1(uint8_t code) {
+  static const float magnitude[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  const float m = magnitude[code & 7];
+  return (code & 8) ? -m : m;
+}
+
+/* Nearest E2M1 code, ties to the even code (even mantissa bit), saturating at 6; NaN -> 0. */
+uint8_t oracle_e2m1_from_f32(float value) {
+  if (value != value) return 0;
+  const uint8_t sign = signbit(value) ? 8 : 0;
+  const float a = fabsf(value);
+  uint8_t best = 7;
+  if (a < 6.0f) {
+    /* The two neighbours in the table; midpoints go to the even code. */
+    for (uint8_t c = 0; c < 7; ++c) {
+      const float lo = oracle_f32_from_e2m1(c), hi = oracle_f32_from_e2m1((uint8_t)(c + 1));
+      if (a >= lo && a <= hi) {
+        const float mid = 0.5f * (lo + hi);
+        if (a < mid) best = c;
+        else if (a > mid) best = (uint8_t)(c + 1);
+        else best = (c & 1) ? (uint8_t)(c + 1) : c;
+        break;
+      }
+    }
+  }
+  return (uint8_t)(sign | best);
+}
+
+/* The E8M0 scale byte of a block: the smallest power of two 2^e with amax <= limit * 2^e (no
+ * element saturates), e clamped to [-127, 127]; an all-zero (or non-finite) block takes 2^0. */
+uint8_t oracle_mx_scale(float amax, float limit) {
+  if (!(amax > 0.0f) || isinf(amax)) return 127;
+  int e;
+  frexpf(amax / limit, &e);                      /* amax / limit in [2^(e-1), 2^e) */
+  while (e > -127 && amax <= ldexpf(limit, e - 1)) --e;
+  while (e < 127 && amax > ldexpf(limit, e)) ++e;
+  return (uint8_t)(e + 127);
+}
+
+static float mx_power(uint8_t x) { return ldexpf(1.0f, (int)x - 127); }
+
+/* Per row, per 32 channels: s = oracle_mx_scale(amax, 448), q = e4m3(x / 2^(s-127)). */
+void oracle_quantize_rows_mxfp8(const uint16_t *in_bf16, int64_t rows, int64_t width, uint8_t *out,
+                                uint8_t *scales) {
+  const int64_t blocks = width / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t b = 0; b < blocks; ++b) {
+      const uint16_t *x = in_bf16 + r * width + b * 32;
+      float amax = 0.0f;
+      for (int64_t i = 0; i < 32; ++i) {
+        const float a = fabsf(oracle_f32_from_bf16(x[i]));
+        amax = a > amax ? a : amax;
+      }
+      const uint8_t s = oracle_mx_scale(amax, 448.0f);
+      scales[r * blocks + b] = s;
+      const float power = mx_power(s);
+      for (int64_t i = 0; i < 32; ++i) out[r * width + b * 32 + i] = oracle_e4m3_from_f32(oracle_f32_from_bf16(x[i]) / power);
+    }
+  }
+}
+
+/* [stacks, n, k] bf16 -> E2M1 pairs [stacks, n, k / 2] (low nibble = lower k) and E8M0 scales
+ * [stacks, n, k / 32], s = oracle_mx_scale(amax, 6). */
+void oracle_quantize_blocks_mxfp4(const uint16_t *in_bf16, int64_t stacks, int64_t n, int64_t k,
+                                  uint8_t *out, uint8_t *scales) {
+  const int64_t blocks = k / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t row = 0; row < stacks * n; ++row) {
+    for (int64_t b = 0; b < blocks; ++b) {
+      const uint16_t *x = in_bf16 + row * k + b * 32;
+      float amax = 0.0f;
+      for (int64_t i = 0; i < 32; ++i) {
+        const float a = fabsf(oracle_f32_from_bf16(x[i]));
+        amax = a > amax ? a : amax;
+      }
+      const uint8_t s = oracle_mx_scale(amax, 6.0f);
+      scales[row * blocks + b] = s;
+      const float power = mx_power(s);
+      for (int64_t i = 0; i < 32; i += 2) {
+        const uint8_t lo = oracle_e2m1_from_f32(oracle_f32_from_bf16(x[i]) / power);
+        const uint8_t hi = oracle_e2m1_from_f32(oracle_f32_from_bf16(x[i + 1]) / power);
+        out[row * (k / 2) + (b * 32 + i) / 2] = (uint8_t)(lo | (hi << 4));
+      }
+    }
+  }
+}
+
+/* Dot of an MXFP8 row and an MXFP4 row over k: per 32-block the FP32 sum of code products (in
+ * order), times both blocks' powers of two; the blocks summed in order. */
+static float dot_mx(const uint8_t *a, const uint8_t *sa, const uint8_t *w, const uint8_t *sw, int64_t k) {
+  float total = 0.0f;
+  for (int64_t b = 0; b < k / 32; ++b) {
+    float partial = 0.0f;
+    for (int64_t i = 0; i < 32; ++i) {
+      const int64_t at = b * 32 + i;
+      const uint8_t code = (uint8_t)((w[at / 2] >> (4 * (at & 1))) & 15);
+      partial += oracle_f32_from_e4m3(a[at]) * oracle_f32_from_e2m1(code);
+    }
+    total += partial * (mx_power(sa[b]) * mx_power(sw[b]));
+  }
+  return total;
+}
+
+void oracle_gather_gemm_mx(const uint8_t *hidden, const uint8_t *hidden_scales, const uint8_t *weights,
+                           const uint8_t *weight_scales, int64_t tokens, int64_t hidden_size,
+                           int64_t intermediate, int64_t top, int64_t tile, const int32_t *tile_to_expert,
+                           const int32_t *tile_to_limit, const int32_t *permuted_to_expanded,
+                           int32_t num_tiles, float *out) {
+  (void)tokens;
+  const int64_t width = 2 * intermediate, kb = hidden_size / 32;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int32_t t = 0; t < num_tiles; ++t) {
+    const int64_t e = tile_to_expert[t];
+    for (int64_t p = (int64_t)t * tile; p < tile_to_limit[t]; ++p) {
+      const int64_t token = permuted_to_expanded[p] / top;
+      for (int64_t n = 0; n < intermediate; ++n) {
+        float v[2];
+        for (int half = 0; half < 2; ++half) {
+          const int64_t row = e * width + n + half * intermediate;
+          v[half] = dot_mx(hidden + token * hidden_size, hidden_scales + token * kb, weights + row * (hidden_size / 2),
+                           weight_scales + row * kb, hidden_size);
+        }
+        out[p * intermediate + n] = silu(v[1]) * v[0];
+      }
+    }
+  }
+}
+
+void oracle_route_gemm_mx(const uint8_t *rows, const uint8_t *row_scales, const uint8_t *weights,
+                          const uint8_t *weight_scales, int64_t hidden_size, int64_t intermediate, int64_t tile,
+                          const int32_t *tile_to_expert, const int32_t *tile_to_limit, int32_t num_tiles,
+                          float *out) {
+  const int64_t kb = intermediate / 32;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int32_t t = 0; t < num_tiles; ++t) {
+    const int64_t e = tile_to_expert[t];
+    for (int64_t p = (int64_t)t * tile; p < tile_to_limit[t]; ++p)
+      for (int64_t n = 0; n < hidden_size; ++n) {
+        const int64_t row = e * hidden_size + n;
+        out[p * hidden_size + n] = dot_mx(rows + p * intermediate, row_scales + p * kb,
+                                          weights + row * (intermediate / 2), weight_scales + row * kb, intermediate);
+      }
+  }
+}
+
 /* ---- the composed layer ------------------------------------------------------------------------ */
 
 int32_t oracle_threads(void) {
@@ -698,7 +849,8 @@ int32_t oracle_threads(void) {
 /* MoE::routed (crates/nn/src/modules/moe.rs:770-795) on the CPU: router gemm (bf16 scores) ->
  * topk (renormalised) -> sort -> FC1 (gated rows rounded to bf16) -> FC2 (products rounded to
  * bf16) -> combine (FP32, one rounding into bf16), the reference's rounding points. For e4m3
- * weights the activations of each product are quantised per row per 128 channels first. */
+ * weights (6) the activations of each product are quantised per row per 128 channels first; for
+ * MX weights (7: E2M1 codes, E8M0 scale bytes) per row per 32 channels to MXFP8. */
 int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const void *up_gate,
                          const float *up_gate_scales, const void *down, const float *down_scales,
                          int64_t tokens, int64_t hidden_size, int64_t experts, int64_t top,
@@ -737,6 +889,20 @@ int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const v
     oracle_quantize_rows_fp8(gated_bf16, padded, intermediate, 128, gq, gs);
     oracle_route_gemm_fp8(gq, gs, (const uint8_t *)down, down_scales, hidden_size, intermediate,
                           tile, t2e, t2l, live_tiles, products);
+    free(xq); free(xs); free(gq); free(gs);
+  } else if (weight_dtype == 7) {
+    /* MX: E2M1 weights with E8M0 scales (the scale pointers are bytes), MXFP8 activations. */
+    uint8_t *xq = (uint8_t *)malloc((size_t)(tokens * hidden_size));
+    uint8_t *xs = (uint8_t *)malloc((size_t)(tokens * hidden_size / 32));
+    oracle_quantize_rows_mxfp8(hidden, tokens, hidden_size, xq, xs);
+    oracle_gather_gemm_mx(xq, xs, (const uint8_t *)up_gate, (const uint8_t *)up_gate_scales, tokens, hidden_size,
+                          intermediate, top, tile, t2e, t2l, p2e, live_tiles, gated);
+    oracle_bf16_encode(gated, gated_bf16, (int64_t)padded * intermediate);
+    uint8_t *gq = (uint8_t *)malloc((size_t)(rows * intermediate));
+    uint8_t *gs = (uint8_t *)malloc((size_t)(rows * intermediate / 32));
+    oracle_quantize_rows_mxfp8(gated_bf16, padded, intermediate, gq, gs);
+    oracle_route_gemm_mx(gq, gs, (const uint8_t *)down, (const uint8_t *)down_scales, hidden_size, intermediate,
+                         tile, t2e, t2l, live_tiles, products);
     free(xq); free(xs); free(gq); free(gs);
   } else {
     oracle_gather_gemm(hidden, (const uint16_t *)up_gate, tokens, hidden_size, intermediate, top,

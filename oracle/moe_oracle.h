@@ -85,8 +85,27 @@ void oracle_route_gemm_fp8(const uint8_t *rows, const float *row_scales, const u
                            int64_t tile, const int32_t *tile_to_expert,
                            const int32_t *tile_to_limit, int32_t num_tiles, float *out);
 
+/* ---- OCP MX: MXFP4 weights x MXFP8 activations ------------------------------------------------ */
+float oracle_f32_from_e2m1(uint8_t code);
+uint8_t oracle_e2m1_from_f32(float value);
+uint8_t oracle_mx_scale(float amax, float limit);
+void oracle_quantize_rows_mxfp8(const uint16_t *in_bf16, int64_t rows, int64_t width, uint8_t *out,
+                                uint8_t *scales);
+void oracle_quantize_blocks_mxfp4(const uint16_t *in_bf16, int64_t stacks, int64_t n, int64_t k,
+                                  uint8_t *out, uint8_t *scales);
+void oracle_gather_gemm_mx(const uint8_t *hidden, const uint8_t *hidden_scales, const uint8_t *weights,
+                           const uint8_t *weight_scales, int64_t tokens, int64_t hidden_size,
+                           int64_t intermediate, int64_t top, int64_t tile, const int32_t *tile_to_expert,
+                           const int32_t *tile_to_limit, const int32_t *permuted_to_expanded,
+                           int32_t num_tiles, float *out);
+void oracle_route_gemm_mx(const uint8_t *rows, const uint8_t *row_scales, const uint8_t *weights,
+                          const uint8_t *weight_scales, int64_t hidden_size, int64_t intermediate, int64_t tile,
+                          const int32_t *tile_to_expert, const int32_t *tile_to_limit, int32_t num_tiles,
+                          float *out);
+
 /* ---- the composed layer (the bench's CPU baseline) -------------------------------------------- */
-/* weight_dtype 4 = bf16 (up_gate / down are uint16_t bf16), 6 = e4m3 (uint8_t + scales).
+/* weight_dtype 4 = bf16 (up_gate / down are uint16_t bf16), 6 = e4m3 (uint8_t + f32 scales),
+ * 7 = MX (E2M1 pairs + E8M0 scale bytes passed through the scale pointers).
  * out is bf16 [tokens, hidden]. Returns the number of OpenMP threads used. */
 int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const void *up_gate,
                          const float *up_gate_scales, const void *down, const float *down_scales,

@@ -52,6 +52,13 @@ _sig("oracle_route_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I32, _
 _sig("oracle_moe_layer", [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P], _I32)
 _sig("oracle_threads", [], _I32)
 _sig("oracle_sigmoid_gated_add", [_P, _P, _P, _I64, _I64, _I32])
+_sig("oracle_f32_from_e2m1", [ctypes.c_uint8], ctypes.c_float)
+_sig("oracle_e2m1_from_f32", [ctypes.c_float], ctypes.c_uint8)
+_sig("oracle_mx_scale", [ctypes.c_float, ctypes.c_float], ctypes.c_uint8)
+_sig("oracle_quantize_rows_mxfp8", [_P, _I64, _I64, _P, _P])
+_sig("oracle_quantize_blocks_mxfp4", [_P, _I64, _I64, _I64, _P, _P])
+_sig("oracle_gather_gemm_mx", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P])
+_sig("oracle_route_gemm_mx", [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
 
 KINDS = {np.dtype(np.float32): 0, "bf16": 1, np.dtype(np.float16): 2}
 
@@ -115,6 +122,73 @@ def sigmoid_gated_add(target, update, gate, kind):
     gate = np.ascontiguousarray(gate)
     rows, columns = out.shape
     LIB.oracle_sigmoid_gated_add(_p(out), _p(update), _p(gate), rows, columns, kind)
+    return out
+
+
+def e2m1_decode(code):
+    return LIB.oracle_f32_from_e2m1(int(code))
+
+
+def e2m1_encode(value):
+    return LIB.oracle_e2m1_from_f32(float(value))
+
+
+def mx_scale(amax, limit):
+    return LIB.oracle_mx_scale(float(amax), float(limit))
+
+
+def mx_power(scales):
+    """2^(s - 127) of E8M0 bytes, as float64."""
+    return np.ldexp(1.0, np.asarray(scales, dtype=np.int64) - 127)
+
+
+def quantize_rows_mxfp8(bits):
+    """bf16 bits [rows, width] -> (e4m3 codes [rows, width], E8M0 bytes [rows, width / 32])."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    rows, width = bits.shape
+    out = np.empty((rows, width), dtype=np.uint8)
+    scales = np.empty((rows, width // 32), dtype=np.uint8)
+    LIB.oracle_quantize_rows_mxfp8(_p(bits), rows, width, _p(out), _p(scales))
+    return out, scales
+
+
+def quantize_blocks_mxfp4(bits):
+    """bf16 bits [stacks, n, k] -> (E2M1 pairs [stacks, n, k / 2], E8M0 bytes [stacks, n, k / 32])."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    stacks, n, k = bits.shape
+    out = np.empty((stacks, n, k // 2), dtype=np.uint8)
+    scales = np.empty((stacks, n, k // 32), dtype=np.uint8)
+    LIB.oracle_quantize_blocks_mxfp4(_p(bits), stacks, n, k, _p(out), _p(scales))
+    return out, scales
+
+
+def e2m1_unpack(packed):
+    """E2M1 pairs [..., k / 2] -> codes [..., k] (low nibble first)."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    out = np.empty(packed.shape[:-1] + (packed.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = packed & 15
+    out[..., 1::2] = packed >> 4
+    return out
+
+
+def gather_gemm_mx(hq, hs, wq, ws, top, sort, rows, fill=np.nan):
+    tokens, hidden = hq.shape
+    experts, width, _ = wq.shape
+    out = np.full((rows, width // 2), fill, dtype=np.float32)
+    LIB.oracle_gather_gemm_mx(_p(_c(hq, np.uint8)), _p(_c(hs, np.uint8)), _p(_c(wq, np.uint8)), _p(_c(ws, np.uint8)),
+                              tokens, hidden, width // 2, top, 128, _p(sort["tile_to_expert"]),
+                              _p(sort["tile_to_limit"]), _p(sort["permuted_to_expanded"]),
+                              int(sort["num_non_exiting_tiles"][0]), _p(out))
+    return out
+
+
+def route_gemm_mx(gq, gs, wq, ws, sort, fill=np.nan):
+    rows, intermediate = gq.shape
+    experts, hidden, _ = wq.shape
+    out = np.full((rows, hidden), fill, dtype=np.float32)
+    LIB.oracle_route_gemm_mx(_p(_c(gq, np.uint8)), _p(_c(gs, np.uint8)), _p(_c(wq, np.uint8)), _p(_c(ws, np.uint8)),
+                             hidden, intermediate, 128, _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
+                             int(sort["num_non_exiting_tiles"][0]), _p(out))
     return out
 
 
@@ -252,12 +326,14 @@ def moe_layer(hidden_bits, router_bits, up_gate, down, top, renormalize=True, up
     tokens, hidden = hidden_bits.shape
     experts = router_bits.shape[0]
     intermediate = up_gate.shape[1] // 2
-    fp8 = up_gate.dtype == np.uint8
+    # MX stacks: E2M1 pairs with E8M0 byte scales; e4m3: bytes with f32 scales.
+    mx = up_gate_scales is not None and np.asarray(up_gate_scales).dtype == np.uint8
+    fp8 = up_gate.dtype == np.uint8 and not mx
     out = np.empty((tokens, hidden), dtype=np.uint16)
     ids = np.empty((tokens, top), dtype=np.int32)
     weights = np.empty((tokens, top), dtype=np.float32)
     threads = LIB.oracle_moe_layer(_p(hidden_bits), _p(router_bits), _p(np.ascontiguousarray(up_gate)),
                                    _p(up_gate_scales), _p(np.ascontiguousarray(down)), _p(down_scales),
                                    tokens, hidden, experts, top, intermediate, 1 if renormalize else 0,
-                                   6 if fp8 else 4, _p(out), _p(ids), _p(weights))
+                                   7 if mx else 6 if fp8 else 4, _p(out), _p(ids), _p(weights))
     return out, ids, weights, threads

@@ -574,3 +574,108 @@ def test_sigmoid_gated_add_rounds_once_into_bf16_and_f16():
     sh = 1.0 / (1.0 + np.exp(-gh.astype(np.float64)))
     want_h = (th.astype(np.float64) + sh[:, None] * uh.astype(np.float64)).astype(np.float16)
     assert np.abs(got_h.astype(np.float64) - want_h.astype(np.float64)).max() <= np.abs(want_h).max() * 2.0 ** -10
+
+
+# ---- OCP MX (MXFP4 weights x MXFP8 activations) -----------------------------------------------------
+
+
+def test_e2m1_codec_every_code_and_ties():
+    """Every code round-trips; midpoints go to the even code; saturation at 6; signed zero."""
+    table = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    for code in range(16):
+        want = table[code & 7] * (-1.0 if code & 8 else 1.0)
+        assert O.e2m1_decode(code) == want
+        assert O.e2m1_encode(want) == code or (code == 8 and O.e2m1_encode(-0.0) == 8)
+    ties = {0.25: 0.0, 0.75: 1.0, 1.25: 1.0, 1.75: 2.0, 2.5: 2.0, 3.5: 4.0, 5.0: 4.0}
+    for value, want in ties.items():
+        assert O.e2m1_decode(O.e2m1_encode(value)) == want, value
+        assert O.e2m1_decode(O.e2m1_encode(-value)) == -want, value
+    assert O.e2m1_decode(O.e2m1_encode(1e9)) == 6.0 and O.e2m1_decode(O.e2m1_encode(-7.0)) == -6.0
+    # Nearest: brute force over a grid against the table.
+    for value in np.linspace(-7.0, 7.0, 2801):
+        got = O.e2m1_decode(O.e2m1_encode(value))
+        best = min(abs(abs(value) - t) for t in table)
+        assert abs(abs(got) - abs(value)) == best or abs(value) > 6.0
+
+
+def test_mx_scale_is_the_smallest_power_without_saturation():
+    rng = np.random.default_rng(11)
+    for amax in np.concatenate([rng.lognormal(0.0, 8.0, 500), [1.0, 6.0, 448.0, 448.0 * 2 ** -20]]).astype(np.float32):
+        for limit in (6.0, 448.0):
+            e = O.mx_scale(amax, limit) - 127
+            assert amax <= limit * 2.0 ** e, (amax, limit, e)
+            assert amax > limit * 2.0 ** (e - 1), (amax, limit, e)
+    assert O.mx_scale(0.0, 448.0) == 127 and O.mx_scale(float("inf"), 6.0) == 127
+
+
+def test_mxfp8_rows_match_torch_cast_under_the_scale():
+    """codes = e4m3(x / 2^(s-127)) by torch's round-to-nearest-even cast, s the smallest power."""
+    import torch
+
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((7, 256)) * np.exp(rng.normal(0, 3, (7, 1)))).astype(np.float32)
+    x[2, :32] = 0.0
+    bits = O.bf16_encode(x)
+    codes, scales = O.quantize_rows_mxfp8(bits)
+    values = O.bf16_decode(bits).astype(np.float64)
+    for r in range(7):
+        for b in range(8):
+            block = values[r, b * 32:(b + 1) * 32]
+            assert scales[r, b] == O.mx_scale(np.abs(block).max(), 448.0)
+            want = torch.from_numpy((block / O.mx_power(scales[r, b])).astype(np.float32)).to(torch.float8_e4m3fn)
+            np.testing.assert_array_equal(codes[r, b * 32:(b + 1) * 32], want.view(torch.uint8).numpy())
+
+
+def test_mxfp4_blocks_round_to_the_nearest_code():
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((2, 4, 64)) * 0.02).astype(np.float32)
+    bits = O.bf16_encode(w)
+    packed, scales = O.quantize_blocks_mxfp4(bits)
+    codes = O.e2m1_unpack(packed)
+    values = O.bf16_decode(bits).astype(np.float64)
+    table = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+    for s in range(2):
+        for n in range(4):
+            for b in range(2):
+                block = values[s, n, b * 32:(b + 1) * 32]
+                power = O.mx_power(scales[s, n, b])
+                assert np.abs(block).max() <= 6.0 * power
+                for i, v in enumerate(block):
+                    code = codes[s, n, b * 32 + i]
+                    got = table[code & 7] * (-1 if code & 8 else 1)
+                    assert abs(abs(got) - abs(v) / power) == np.abs(table - abs(v) / power).min()
+
+
+def test_mx_products_against_float64():
+    """FC1 / FC2 over MX operands equal float64 sums of the dequantised values (FP32 rounding)."""
+    rng = np.random.default_rng(14)
+    tokens, hidden, experts, top, intermediate = 12, 256, 4, 2, 128
+    x = O.bf16_encode(rng.standard_normal((tokens, hidden)).astype(np.float32))
+    w1 = O.bf16_encode((rng.standard_normal((experts, 2 * intermediate, hidden)) * 0.05).astype(np.float32))
+    w2 = O.bf16_encode((rng.standard_normal((experts, hidden, intermediate)) * 0.05).astype(np.float32))
+    ids = np.stack([rng.choice(experts, top, replace=False) for _ in range(tokens)]).astype(np.int32)
+    sort = O.moe_sort(ids, experts)
+    rows = O.max_tiles(tokens, top, experts) * 128
+    xq, xs = O.quantize_rows_mxfp8(x)
+    q1, s1 = O.quantize_blocks_mxfp4(w1)
+    q2, s2 = O.quantize_blocks_mxfp4(w2)
+    gated = O.gather_gemm_mx(xq, xs, q1, s1, top, sort, rows, fill=0.0)
+    dx = O.e4m3_decode_array(xq) * np.repeat(O.mx_power(xs), 32, axis=1)
+    table = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+    d1 = table[O.e2m1_unpack(q1)] * np.repeat(O.mx_power(s1), 32, axis=2)
+    d2 = table[O.e2m1_unpack(q2)] * np.repeat(O.mx_power(s2), 32, axis=2)
+    p2e = sort["permuted_to_expanded"]
+    t2e, t2l = sort["tile_to_expert"], sort["tile_to_limit"]
+    for t in range(int(sort["num_non_exiting_tiles"][0])):
+        for p in range(t * 128, t2l[t]):
+            token, e = p2e[p] // top, t2e[t]
+            h = d1[e] @ dx[token]
+            want = h[intermediate:] / (1 + np.exp(-h[intermediate:])) * h[:intermediate]
+            np.testing.assert_allclose(gated[p], want, rtol=1e-4, atol=1e-5 * np.abs(h).max())
+    gq, gs = O.quantize_rows_mxfp8(O.bf16_encode(gated))
+    products = O.route_gemm_mx(gq, gs, q2, s2, sort, fill=0.0)
+    dg = O.e4m3_decode_array(gq) * np.repeat(O.mx_power(gs), 32, axis=1)
+    for t in range(int(sort["num_non_exiting_tiles"][0])):
+        for p in range(t * 128, t2l[t]):
+            want = d2[t2e[t]] @ dg[p]
+            np.testing.assert_allclose(products[p], want, rtol=1e-4, atol=1e-5 * np.abs(want).max())

@@ -1,0 +1,427 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// OCP MX forms of the grouped expert products on gfx950: MXFP4 (E2M1) expert weights times MXFP8
+// (e4m3) activations, both with one E8M0 scale per 32 elements along K, and the MXFP8 activation
+// quantiser. No reference counterpart (its four-bit experts are NVFP4, crates/ops/src/moe/
+// grouped.rs:579-1772, in the same call style).
+//
+// `v_mfma_scale_f32_16x16x128_f8f6f4` takes an E2M1 A operand (cbsz 4, four registers) and an
+// e4m3 B operand (blgp 0, eight registers), plus one E8M0 scale byte per lane for each. Measured on
+// this GPU (single-element and scale-doubling probes): lane l = 16 g + r supplies, for row / column
+// r, the E2M1 elements K 32 g .. 32 g + 31 (16 bytes, lower K in the low nibble) and the e4m3
+// elements K 16 g .. 16 g + 15 and 64 + 16 g .. 64 + 16 g + 15 (two 16-byte pieces); its scale byte
+// is that of row / column r's block g (K 32 g .. 32 g + 31), whichever lanes hold the block's data.
+// So the hardware applies both MX block scales itself and the products accumulate straight into
+// the FP32 accumulator: no per-block scaling on the VALU.
+//
+// The product kernel is the decode-shaped stream kernel of the e4m3 products (one tile x a slice of
+// weight rows per workgroup; weights streamed as whole 128-byte lines, non-temporal, and regrouped
+// into the MFMA layout with ds_bpermute), walking K 256 elements (one 128-byte weight line) at a
+// time; at prefill shapes it takes each tile in passes of 16 tokens.
+#include "common.hpp"
+#include "grouped_fp8.hpp"
+#include "uniserve_moe_mx.h"
+
+namespace uniserve {
+namespace {
+
+// ---- the MXFP8 quantiser -------------------------------------------------------------------------------
+
+constexpr int kQuantThreads = 256;
+
+struct MxQuantParams {
+  const void *input;
+  uint8_t *out;
+  uint8_t *scales;
+  const int32_t *row_limit;
+  int64_t rows;
+  int64_t width;
+  int32_t input_f32;
+};
+
+/// The E8M0 byte of a block: the smallest power of two 2^e with amax <= limit * 2^e, e in
+/// [-127, 127]; an all-zero or infinite block takes 2^0. The division is IEEE (the library is
+/// built with correctly rounded division) and the comparisons are exact, so the host rule holds
+/// bit for bit.
+__device__ __forceinline__ uint32_t mx_scale(float amax, float limit) {
+  if (!(amax > 0.0f) || __builtin_isinf(amax)) return 127u;
+  int e;
+  frexpf(amax / limit, &e);
+  while (e > -127 && amax <= ldexpf(limit, e - 1)) --e;
+  while (e < 127 && amax > ldexpf(limit, e)) ++e;
+  return static_cast<uint32_t>(e + 127);
+}
+
+/// Four lanes per 32-channel block, eight channels each; a grid-stride loop that stops at the
+/// device-side row limit.
+__global__ void __launch_bounds__(kQuantThreads) quantize_mxfp8_kernel(MxQuantParams p) {
+  const int64_t blocks_per_row = p.width / 32;
+  const int sub = static_cast<int>(threadIdx.x) & 3;
+  const int64_t limit = p.row_limit != nullptr ? p.row_limit[0] : p.rows;
+  const int64_t last = (limit < p.rows ? limit : p.rows) * blocks_per_row;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kQuantThreads / 4;
+  for (int64_t block = (static_cast<int64_t>(blockIdx.x) * kQuantThreads + threadIdx.x) / 4; block < last;
+       block += stride) {
+    const int64_t row = block / blocks_per_row;
+    const int64_t column = (block % blocks_per_row) * 32 + sub * 8;
+    float v[8];
+    if (p.input_f32) {
+      const float *src = static_cast<const float *>(p.input) + row * p.width + column;
+      const float4 lo = *reinterpret_cast<const float4 *>(src);
+      const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
+      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    } else {
+      const u32x4 packed = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p.input) + row * p.width + column);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(packed[j] << 16);
+        v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 4));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
+    const uint32_t scale = mx_scale(amax, 448.0f);
+    // A power of two: the division is exact and no quotient exceeds 448.
+    *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, ldexpf(1.0f, static_cast<int>(scale) - 127));
+    if (sub == 0) p.scales[block] = static_cast<uint8_t>(scale);
+  }
+}
+
+// ---- the products ----------------------------------------------------------------------------------------------
+
+constexpr int kTileRows = 128;
+constexpr int kThreads = 256;
+constexpr int kPassTiles = 1;           // 16-token MFMA blocks per pass (one keeps two waves per SIMD)
+constexpr int64_t kSplitBelow = 512;    // workgroups under which K is split over the waves
+
+struct MxParams {
+  const uint8_t *act;            ///< FC1: [tokens, K] e4m3; FC2: [permuted_rows, K]
+  const uint8_t *act_scales;     ///< [rows of act, K / 32] E8M0
+  const uint8_t *weights;        ///< [experts, n_total, K / 2] E2M1 pairs
+  const uint8_t *weight_scales;  ///< [experts, n_total, K / 32] E8M0
+  uint16_t *out;                 ///< [permuted_rows, out_width] bf16
+  const int32_t *tile_to_expert;
+  const int32_t *tile_to_limit;
+  const int32_t *permuted_to_expanded;
+  const int32_t *num_tiles;
+  int64_t K;
+  int64_t n_total;
+  int64_t out_width;
+  int64_t top;
+};
+
+__device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
+  uint2 packed;
+  packed.x = pack_bf16x2(v[0], v[1]);
+  packed.y = pack_bf16x2(v[2], v[3]);
+  *reinterpret_cast<uint2 *>(pointer) = packed;
+}
+
+/// The 16 bytes lane `source` holds in `value` (ds_bpermute).
+__device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
+  u32x4 out;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    out[d] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(source * 4, static_cast<int>(value[d])));
+  return out;
+}
+
+/// D += (E2M1 A scaled by 2^(sa - 127)) . (e4m3 B scaled by 2^(sb - 127)) over 128 K; the scales
+/// are this lane's bytes (its row and its 32 K elements).
+__device__ __forceinline__ floatx4 mfma_mx(const u32x4 &a, const intx8 &b, uint32_t sa, uint32_t sb, floatx4 c) {
+  const intx8 a8 = intx8{static_cast<int>(a[0]), static_cast<int>(a[1]), static_cast<int>(a[2]), static_cast<int>(a[3]),
+                         0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b, c, 4, 0, 0, static_cast<int>(sa), 0,
+                                                          static_cast<int>(sb));
+}
+
+/// One tile x a slice of weight rows per workgroup; each wave owns two sets of 16 weight rows
+/// (FC1: 16 up rows and the matching 16 gate rows; FC2: 32 consecutive rows). K walks in 256-element
+/// chunks: one 128-byte line of each weight row, i.e. two 16x16x128 MFMAs per set (h = 0, 1).
+/// kSplit: the four waves share one row set and split the chunks (chunk c to wave c % 4), their
+/// partial sums meeting in LDS in wave order - for batches too small to fill the chip otherwise.
+template <bool kGated, bool kSplit>
+__global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
+  __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
+  const int tile = static_cast<int>(blockIdx.x);
+  if (tile >= p.num_tiles[0]) return;
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int64_t chunks = p.K / 256;
+  const int64_t weight_row_bytes = p.K / 2;
+  const int64_t scale_row_bytes = p.K / 32;
+
+  int64_t n0, n1;
+  const int row_set = kSplit ? 0 : wave;
+  if constexpr (kGated) {
+    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 16 : 64) + row_set * 16;
+    n1 = p.out_width + n0;
+  } else {
+    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
+    n1 = n0 + 16;
+    if (n0 >= p.out_width) return;
+  }
+  const int64_t c_first = kSplit ? wave : 0;
+  const int64_t c_step = kSplit ? kThreads / kWave : 1;
+  // Weight lines: load i (0..3) of a chunk reads rows 8 (i % 2) + l / 8 of set i / 2, 16-byte piece
+  // l % 8 of the row's 128-byte line. Lane l's A operand for MFMA h (row r16, K 128 h + 32 g ..)
+  // is piece 4 h + g of row r16: gathered with ds_bpermute from load (r16 >= 8) of its set.
+  const uint8_t *line_row[2];
+  line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
+  line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
+  const bool upper = r16 >= 8;
+  const int source0 = (r16 & 7) * 8 + g;  // piece g (MFMA h = 0)
+  const int source1 = source0 + 4;        // piece g + 4 (MFMA h = 1)
+  // This lane's weight scales: its row r16 of each set, eight E8M0 bytes per chunk.
+  const uint8_t *ws[2];
+  ws[0] = p.weight_scales + (expert * p.n_total + n0 + r16) * scale_row_bytes;
+  ws[1] = p.weight_scales + (expert * p.n_total + n1 + r16) * scale_row_bytes;
+
+  for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
+    const uint8_t *a[kPassTiles];
+    const uint8_t *as[kPassTiles];
+    bool valid[kPassTiles];
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      valid[ms] = m < rows;
+      int64_t source = first + m;
+      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      if (!valid[ms]) source = 0;
+      a[ms] = p.act + source * p.K + g * 16;
+      as[ms] = p.act_scales + source * scale_row_bytes;
+    }
+    floatx4 acc[2][kPassTiles];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // One chunk's operands: four weight lines, two 8-byte weight-scale words, and per token block
+    // 64 activation bytes (two MFMAs' worth: pieces g and g + 4 of each 128-byte half) and an
+    // 8-byte activation-scale word.
+    struct Chunk {
+      u32x4 lines[4];
+      uint2 wscale[2];
+      intx8 x[kPassTiles][2];
+      uint2 xscale[kPassTiles];
+    };
+    auto fetch = [&](int64_t c, Chunk &d) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        d.lines[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * weight_row_bytes + c * 128));
+#pragma unroll
+      for (int s = 0; s < 2; ++s) d.wscale[s] = *reinterpret_cast<const uint2 *>(ws[s] + c * 8);
+#pragma unroll
+      for (int ms = 0; ms < kPassTiles; ++ms) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (valid[ms]) {
+            const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + c * 256 + h * 128);
+            const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + c * 256 + h * 128 + 64);
+            d.x[ms][h] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                               static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+          } else {
+            d.x[ms][h] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+        }
+        d.xscale[ms] = valid[ms] ? *reinterpret_cast<const uint2 *>(as[ms] + c * 8) : uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
+      }
+    };
+    // Byte 4 h + g of an 8-byte scale word: this lane's block of MFMA h.
+    auto scale_byte = [&](const uint2 &word, int h) -> uint32_t { return ((h == 0 ? word.x : word.y) >> (8 * g)) & 0xffu; };
+    auto compute = [&](const Chunk &d) {
+#pragma unroll
+      for (int set = 0; set < 2; ++set) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          // Every lane takes part in both permutes; the select picks its row's load.
+          const int source = h == 0 ? source0 : source1;
+          const u32x4 from_lo = permute16(source, d.lines[2 * set]);
+          const u32x4 from_hi = permute16(source, d.lines[2 * set + 1]);
+          const u32x4 w = upper ? from_hi : from_lo;
+          const uint32_t sw = scale_byte(d.wscale[set], h);
+#pragma unroll
+          for (int ms = 0; ms < kPassTiles; ++ms)
+            acc[set][ms] = mfma_mx(w, d.x[ms][h], sw, scale_byte(d.xscale[ms], h), acc[set][ms]);
+        }
+      }
+    };
+    Chunk cur, next;
+    if (c_first < chunks) fetch(c_first, cur);
+    for (int64_t c = c_first; c < chunks; c += 2 * c_step) {
+      if (c + c_step < chunks) fetch(c + c_step, next);
+      compute(cur);
+      if (c + 2 * c_step < chunks) fetch(c + 2 * c_step, cur);
+      if (c + c_step < chunks) compute(next);
+    }
+    if constexpr (kSplit) {
+      // Waves 1..3 hand their partial sums to wave 0, which adds them in wave order.
+      if (wave > 0) {
+#pragma unroll
+        for (int set = 0; set < 2; ++set)
+#pragma unroll
+          for (int ms = 0; ms < kPassTiles; ++ms) partial[wave - 1][set][ms][lane] = acc[set][ms];
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < kThreads / kWave - 1; ++w)
+#pragma unroll
+          for (int set = 0; set < 2; ++set)
+#pragma unroll
+            for (int ms = 0; ms < kPassTiles; ++ms) acc[set][ms] += partial[w][set][ms][lane];
+      }
+      __syncthreads();
+      if (wave > 0) continue;
+    }
+
+#pragma unroll
+    for (int ms = 0; ms < kPassTiles; ++ms) {
+      const int m = pass + ms * 16 + r16;
+      if (m >= rows) continue;
+      uint16_t *row = p.out + (first + m) * p.out_width;
+      if constexpr (kGated) {
+        floatx4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        store_bf16x4(row + n0 + 4 * g, v);
+      } else {
+        store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
+        store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
+      }
+    }
+  }
+}
+
+void launch_mx(const MxParams &p, bool gated, int64_t max_tiles, hipStream_t stream) {
+  const int64_t slices = gated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
+  if (max_tiles * slices < kSplitBelow) {
+    const int64_t split_slices = gated ? p.out_width / 16 : ceil_div<int64_t>(p.out_width, 32);
+    const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(split_slices));
+    if (gated) hipLaunchKernelGGL((stream_mx_kernel<true, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((stream_mx_kernel<false, true>), grid, dim3(kThreads), 0, stream, p);
+    return;
+  }
+  const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices));
+  if (gated) hipLaunchKernelGGL((stream_mx_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((stream_mx_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+}
+
+}  // namespace
+
+void launch_quantize_mxfp8(const void *input, bool input_f32, uint8_t *out, uint8_t *scales,
+                           const int32_t *row_limit, int64_t rows, int64_t width, hipStream_t stream) {
+  MxQuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0};
+  const int64_t blocks = ceil_div<int64_t>(rows * (width / 32) * 4, kQuantThreads);
+  const uint32_t grid = static_cast<uint32_t>(blocks < 2048 ? (blocks > 0 ? blocks : 1) : 2048);
+  hipLaunchKernelGGL(quantize_mxfp8_kernel, dim3(grid), dim3(kQuantThreads), 0, stream, p);
+}
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_quantize_mxfp8(const uniserve_quantize_mxfp8_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->input == nullptr || call->out == nullptr || call->scales == nullptr)
+      return UNISERVE_REFUSE(call, "quantize_mxfp8 needs input, out and scales");
+    if (call->width <= 0 || call->width % 128 != 0)
+      return UNISERVE_REFUSE(call, "quantize_mxfp8 needs a width of whole 128-channel groups");
+    if (call->input_dtype != UNISERVE_DTYPE_BF16 && call->input_dtype != UNISERVE_DTYPE_F32)
+      return UNISERVE_REFUSE(call, "quantize_mxfp8 reads bf16 or f32 rows");
+    if (call->rows < 0) return UNISERVE_REFUSE(call, "quantize_mxfp8 needs a non-negative row count");
+    if (call->rows == 0) return 0;
+    launch_quantize_mxfp8(call->input, call->input_dtype == UNISERVE_DTYPE_F32, static_cast<uint8_t *>(call->out),
+                          call->scales, call->row_limit, call->rows, call->width, static_cast<hipStream_t>(stream));
+    return launched(call, "quantize_mxfp8");
+  });
+}
+
+extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_mx writes bf16 only");
+    if (call->hidden == nullptr || call->hidden_scales == nullptr || call->weights == nullptr ||
+        call->weight_scales == nullptr || call->out == nullptr)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx needs hidden, weights, their scales and out");
+    if (call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->permuted_to_expanded == nullptr || call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx needs the sort's tile and route maps");
+    if (call->multiprocessors <= 0) return UNISERVE_REFUSE(call, "gather_gemm_mx needs its device's multiprocessor count");
+    if (call->hidden_size <= 0 || call->hidden_size % 256 != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx needs a hidden size of whole 256-element chunks");
+    if (call->width <= 0 || call->width % 128 != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx needs an intermediate width of whole 64-column slices");
+    if (call->tokens < 0 || call->top <= 0 || call->experts <= 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx needs non-negative tokens and positive top and experts");
+    if (call->permuted_rows < call->tokens * call->top || call->permuted_rows % kTileRows != 0)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx needs whole 128-row tiles that hold every route");
+    const int64_t max_tiles = call->permuted_rows / kTileRows;
+    if (max_tiles == 0) return 0;
+    MxParams p{};
+    p.act = static_cast<const uint8_t *>(call->hidden);
+    p.act_scales = call->hidden_scales;
+    p.weights = static_cast<const uint8_t *>(call->weights);
+    p.weight_scales = call->weight_scales;
+    p.out = static_cast<uint16_t *>(call->out);
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.num_tiles = call->num_non_exiting_tiles;
+    p.K = call->hidden_size;
+    p.n_total = call->width;
+    p.out_width = call->width / 2;
+    p.top = call->top;
+    launch_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
+    return launched(call, "gather_gemm_mx");
+  });
+}
+
+extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "route_gemm_mx writes bf16 only");
+    if (call->rows == nullptr || call->row_scales == nullptr || call->weights == nullptr ||
+        call->weight_scales == nullptr || call->out == nullptr)
+      return UNISERVE_REFUSE(call, "route_gemm_mx needs rows, weights, their scales and out");
+    if (call->tile_to_expert == nullptr || call->tile_to_limit == nullptr ||
+        call->permuted_to_expanded == nullptr || call->num_non_exiting_tiles == nullptr)
+      return UNISERVE_REFUSE(call, "route_gemm_mx needs the sort's tile and route maps");
+    if (call->multiprocessors <= 0) return UNISERVE_REFUSE(call, "route_gemm_mx needs its device's multiprocessor count");
+    if (call->intermediate <= 0 || call->intermediate % 256 != 0)
+      return UNISERVE_REFUSE(call, "route_gemm_mx needs an intermediate width of whole 256-element chunks");
+    if (call->width <= 0 || call->width % 32 != 0)
+      return UNISERVE_REFUSE(call, "route_gemm_mx needs a hidden width of whole 32-row sets");
+    if (call->experts <= 0) return UNISERVE_REFUSE(call, "route_gemm_mx needs positive experts");
+    if (call->permuted_rows < 0 || call->permuted_rows % kTileRows != 0)
+      return UNISERVE_REFUSE(call, "route_gemm_mx needs permuted rows of whole 128-row tiles");
+    const int64_t max_tiles = call->permuted_rows / kTileRows;
+    if (max_tiles == 0) return 0;
+    MxParams p{};
+    p.act = static_cast<const uint8_t *>(call->rows);
+    p.act_scales = call->row_scales;
+    p.weights = static_cast<const uint8_t *>(call->weights);
+    p.weight_scales = call->weight_scales;
+    p.out = static_cast<uint16_t *>(call->out);
+    p.tile_to_expert = call->tile_to_expert;
+    p.tile_to_limit = call->tile_to_limit;
+    p.permuted_to_expanded = call->permuted_to_expanded;
+    p.num_tiles = call->num_non_exiting_tiles;
+    p.K = call->intermediate;
+    p.n_total = call->width;
+    p.out_width = call->width;
+    p.top = 1;
+    launch_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
+    return launched(call, "route_gemm_mx");
+  });
+}

@@ -15,6 +15,9 @@ from .abi import (  # noqa: F401
     LayerCall,
     LayerViews,
     QuantizeFp8Call,
+    QuantizeMxfp8Call,
+    GatherMxCall,
+    RouteMxCall,
     RouteCall,
     RouteFp8Call,
     SortCall,

@@ -208,6 +208,69 @@ class RouteFp8Call(ctypes.Structure):
     ]
 
 
+class QuantizeMxfp8Call(ctypes.Structure):
+    """``uniserve_quantize_mxfp8_call``."""
+
+    _fields_ = [
+        ("input", _P),
+        ("out", _P),
+        ("scales", _P),
+        ("row_limit", _P),
+        ("rows", _I64),
+        ("width", _I64),
+        ("input_dtype", _I64),
+        ("error", _ERR),
+    ]
+
+
+class GatherMxCall(ctypes.Structure):
+    """``uniserve_gather_mx_call``."""
+
+    _fields_ = [
+        ("hidden", _P),
+        ("hidden_scales", _P),
+        ("weights", _P),
+        ("weight_scales", _P),
+        ("out", _P),
+        ("tile_to_expert", _P),
+        ("tile_to_limit", _P),
+        ("permuted_to_expanded", _P),
+        ("num_non_exiting_tiles", _P),
+        ("tokens", _I64),
+        ("permuted_rows", _I64),
+        ("width", _I64),
+        ("hidden_size", _I64),
+        ("experts", _I64),
+        ("top", _I64),
+        ("out_dtype", _I64),
+        ("multiprocessors", _I64),
+        ("error", _ERR),
+    ]
+
+
+class RouteMxCall(ctypes.Structure):
+    """``uniserve_route_mx_call``."""
+
+    _fields_ = [
+        ("rows", _P),
+        ("row_scales", _P),
+        ("weights", _P),
+        ("weight_scales", _P),
+        ("out", _P),
+        ("tile_to_expert", _P),
+        ("tile_to_limit", _P),
+        ("permuted_to_expanded", _P),
+        ("num_non_exiting_tiles", _P),
+        ("permuted_rows", _I64),
+        ("width", _I64),
+        ("intermediate", _I64),
+        ("experts", _I64),
+        ("out_dtype", _I64),
+        ("multiprocessors", _I64),
+        ("error", _ERR),
+    ]
+
+
 class LayerCall(ctypes.Structure):
     """``uniserve_moe_layer_call``."""
 
@@ -304,6 +367,9 @@ _ENTRIES = {
     "uniserve_gather_gemm_fp8": GatherFp8Call,
     "uniserve_route_gemm_fp8": RouteFp8Call,
     "uniserve_moe_layer": LayerCall,
+    "uniserve_quantize_mxfp8": QuantizeMxfp8Call,
+    "uniserve_gather_gemm_mx": GatherMxCall,
+    "uniserve_route_gemm_mx": RouteMxCall,
 }
 
 

@@ -20,6 +20,9 @@ from .abi import (
     LayerCall,
     LayerViews,
     QuantizeFp8Call,
+    QuantizeMxfp8Call,
+    GatherMxCall,
+    RouteMxCall,
     RouteCall,
     RouteFp8Call,
     SortCall,
@@ -251,6 +254,60 @@ def route_gemm_fp8(gated_q, gated_s, down_q, down_s, maps, out=None):
     call.experts, call.block_n, call.block_k = experts, 128, 128
     call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(gated_q.device)
     _check(library().uniserve_route_gemm_fp8(ctypes.byref(call), _stream(gated_q.device)), call, "route_gemm_fp8")
+    return out
+
+
+def quantize_mxfp8(rows_tensor, row_limit=None):
+    """Per-row, per-32-channel MXFP8: e4m3 codes (uint8) and E8M0 scale bytes (uint8)."""
+    rows, width = rows_tensor.shape
+    out = torch.empty((rows, width), dtype=torch.uint8, device=rows_tensor.device)
+    scales = torch.empty((rows, width // 32), dtype=torch.uint8, device=rows_tensor.device)
+    call = QuantizeMxfp8Call()
+    call.input, call.out, call.scales = rows_tensor.data_ptr(), out.data_ptr(), scales.data_ptr()
+    call.row_limit = _ptr(row_limit)
+    call.rows, call.width = rows, width
+    call.input_dtype = DTYPE[_TORCH_DTYPE[rows_tensor.dtype]]
+    _check(library().uniserve_quantize_mxfp8(ctypes.byref(call), _stream(rows_tensor.device)), call, "quantize_mxfp8")
+    return out, scales
+
+
+def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None):
+    """FC1 over MXFP8 tokens and MXFP4 weights (``up_gate_q`` [E, 2I, H / 2] E2M1 pairs)."""
+    tokens, width = hidden_q.shape
+    experts, gated, _ = up_gate_q.shape
+    if out is None:
+        out = torch.empty((rows, gated // 2), dtype=torch.bfloat16, device=hidden_q.device)
+    call = GatherMxCall()
+    call.hidden, call.hidden_scales = hidden_q.data_ptr(), hidden_s.data_ptr()
+    call.weights, call.weight_scales, call.out = up_gate_q.data_ptr(), up_gate_s.data_ptr(), out.data_ptr()
+    call.tile_to_expert = maps[TILE_TO_EXPERT].data_ptr()
+    call.tile_to_limit = maps[TILE_TO_LIMIT].data_ptr()
+    call.permuted_to_expanded = maps[PERMUTED_TO_EXPANDED].data_ptr()
+    call.num_non_exiting_tiles = maps[NUM_NON_EXITING_TILES].data_ptr()
+    call.tokens, call.permuted_rows, call.width, call.hidden_size = tokens, rows, gated, width
+    call.experts, call.top = experts, top
+    call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(hidden_q.device)
+    _check(library().uniserve_gather_gemm_mx(ctypes.byref(call), _stream(hidden_q.device)), call, "gather_gemm_mx")
+    return out
+
+
+def route_gemm_mx(gated_q, gated_s, down_q, down_s, maps, out=None):
+    """FC2 over MXFP8 rows and MXFP4 weights (``down_q`` [E, H, I / 2] E2M1 pairs)."""
+    rows, intermediate = gated_q.shape
+    experts, hidden, _ = down_q.shape
+    if out is None:
+        out = torch.empty((rows, hidden), dtype=torch.bfloat16, device=gated_q.device)
+    call = RouteMxCall()
+    call.rows, call.row_scales = gated_q.data_ptr(), gated_s.data_ptr()
+    call.weights, call.weight_scales, call.out = down_q.data_ptr(), down_s.data_ptr(), out.data_ptr()
+    call.tile_to_expert = maps[TILE_TO_EXPERT].data_ptr()
+    call.tile_to_limit = maps[TILE_TO_LIMIT].data_ptr()
+    call.permuted_to_expanded = maps[PERMUTED_TO_EXPANDED].data_ptr()
+    call.num_non_exiting_tiles = maps[NUM_NON_EXITING_TILES].data_ptr()
+    call.permuted_rows, call.width, call.intermediate = rows, hidden, intermediate
+    call.experts = experts
+    call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(gated_q.device)
+    _check(library().uniserve_route_gemm_mx(ctypes.byref(call), _stream(gated_q.device)), call, "route_gemm_mx")
     return out
 
 
