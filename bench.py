@@ -24,7 +24,8 @@ sys.path.insert(0, str(ROOT / "uniserve-v1_amd"))
 
 METRIC = "MoE-layer tokens/s + % of HBM (decode) / MFMA (prefill) roofline, 1 GPU"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f8e4m3": 5000.0}  # dense
+# Dense peaks; an MXFP4 x MXFP8 scaled MFMA runs at the fp8 rate (its B operand is e4m3).
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f8e4m3": 5000.0, "f4e2m1": 5000.0}
 
 CONFIGS = {
     # name: tokens, hidden, experts, top, intermediate, weights, zipf routing
@@ -34,6 +35,10 @@ CONFIGS = {
     "30b-prefill-fp8": (8192, 2048, 128, 8, 768, "f8e4m3", True),
     "235b-prefill-fp8": (4096, 4096, 128, 8, 1536, "f8e4m3", True),
     "235b-decode-fp8": (1, 4096, 128, 8, 1536, "f8e4m3", False),
+    "30b-decode-mx": (64, 2048, 128, 8, 768, "f4e2m1", False),
+    "30b-prefill-mx": (8192, 2048, 128, 8, 768, "f4e2m1", True),
+    "235b-decode-mx": (1, 4096, 128, 8, 1536, "f4e2m1", False),
+    "235b-prefill-mx": (4096, 4096, 128, 8, 1536, "f4e2m1", True),
 }
 
 
@@ -62,7 +67,7 @@ class Workload:
         import torch
 
         from uniserve_moe import ops
-        from uniserve_moe.checkpoint import quantize_blocks_e4m3
+        from uniserve_moe.checkpoint import quantize_blocks_e4m3, quantize_blocks_mxfp4
 
         self.name = name
         (self.tokens, self.hidden, self.experts, self.top, self.intermediate, self.wdtype,
@@ -86,6 +91,11 @@ class Workload:
             # Setup, not timed: 128 x 128 block-scaled e4m3 (scale = blockmax / 448).
             self.up_gate, s1 = quantize_blocks_e4m3(self.up_gate_bf16)
             self.down, s2 = quantize_blocks_e4m3(self.down_bf16)
+            self.scales = dict(up_gate_scales=s1, down_scales=s2)
+        elif self.wdtype == "f4e2m1":
+            # Setup, not timed: OCP MXFP4 (E2M1 pairs, an E8M0 scale per 32 along K).
+            self.up_gate, s1 = quantize_blocks_mxfp4(self.up_gate_bf16)
+            self.down, s2 = quantize_blocks_mxfp4(self.down_bf16)
             self.scales = dict(up_gate_scales=s1, down_scales=s2)
         else:
             self.up_gate, self.down = self.up_gate_bf16, self.down_bf16
@@ -140,18 +150,19 @@ def algorithmic(w):
     ids = w.layer.view("ids", torch.int32, (w.tokens, w.top)).cpu()
     touched = int(torch.unique(ids).numel())
     routes = w.tokens * w.top
-    elem = 1 if w.wdtype == "f8e4m3" else 2
+    # Bytes per weight element (MXFP4: half a byte plus an E8M0 byte per 32 elements).
+    elem = {"bf16": 2, "f8e4m3": 1, "f4e2m1": 0.5 + 1 / 32}[w.wdtype]
     H, I, E, T = w.hidden, w.intermediate, w.experts, w.tokens
     scale_bytes = 0
     if w.wdtype == "f8e4m3":
         scale_bytes = touched * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128)) * 4
-    layer_bytes = touched * 3 * H * I * elem + scale_bytes + T * H * 2 * 2 + H * E * 2
+    layer_bytes = int(touched * 3 * H * I * elem) + scale_bytes + T * H * 2 * 2 + H * E * 2
     layer_flops = 2 * routes * 3 * H * I + 2 * T * H * E
-    act_elem = 1 if w.wdtype == "f8e4m3" else 2
+    act_elem = {"bf16": 2, "f8e4m3": 1, "f4e2m1": 1 + 1 / 32}[w.wdtype]
     # FC1 writes the gated rows in bf16, or (e4m3 prefill shapes) as e4m3 codes with a scale per
     # 128 columns.
     gated_elem = 1 + 4 / 128 if w.wdtype == "f8e4m3" and w.layer.views.route_scales else 2
-    fc1_bytes = touched * 2 * I * H * elem + T * H * act_elem + int(routes * I * gated_elem)
+    fc1_bytes = int(touched * 2 * I * H * elem + T * H * act_elem + routes * I * gated_elem)
     if w.wdtype == "f8e4m3":
         fc1_bytes += touched * (2 * I // 128) * (H // 128) * 4 + T * (H // 128) * 4
     fc1_flops = 2 * routes * 2 * I * H
@@ -171,7 +182,7 @@ def cpu_baseline(w, runs):
         return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
     x, router = bits(w.x), bits(w.router)
-    if w.wdtype == "f8e4m3":
+    if w.wdtype in ("f8e4m3", "f4e2m1"):
         up_gate, down = w.up_gate.cpu().numpy(), w.down.cpu().numpy()
         s1 = w.scales["up_gate_scales"].cpu().numpy()
         s2 = w.scales["down_scales"].cpu().numpy()
@@ -328,7 +339,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if w.wdtype == "bf16" else "fp8-e4m3 (bf16 out)",
+        "dtype": {"bf16": "bf16", "f8e4m3": "fp8-e4m3 (bf16 out)",
+                  "f4e2m1": "mxfp4 weights x mxfp8 activations (bf16 out)"}[w.wdtype],
         "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) weights)",
         "config": {"workload": f"Qwen3-MoE layer {args.config}", "tokens": w.tokens, "hidden": w.hidden,
                    "experts": w.experts, "top": w.top, "intermediate": w.intermediate,

@@ -9,7 +9,11 @@
 // weight_dtype BF16: `up_gate` [E, 2I, H] (up rows then gate rows) and `down` [E, H, I] in bf16.
 // weight_dtype F8E4M3: both stacks e4m3 with FP32 128x128 block scales
 // (`up_gate_scales` [E, 2I/128, H/128], `down_scales` [E, H/128, I/128]); the activations are
-// quantised per row per 128 channels inside the call. The output is bf16 either way.
+// quantised per row per 128 channels inside the call.
+// weight_dtype F4E2M1 (OCP MXFP4): both stacks E2M1 pairs along K (`up_gate` [E, 2I, H/2],
+// `down` [E, H, I/2]) with one E8M0 byte per 32 K elements (`up_gate_scales` [E, 2I, H/32],
+// `down_scales` [E, H, I/32], passed through the same pointers as bytes); the activations are
+// quantised to MXFP8 inside the call. The output is bf16 in every case.
 
 #pragma once
 
@@ -20,8 +24,8 @@ struct uniserve_moe_layer_call {
   const void *router;          ///< [experts, hidden_size] bf16
   const void *up_gate;         ///< [experts, 2 * intermediate, hidden_size]
   const void *down;            ///< [experts, hidden_size, intermediate]
-  const float *up_gate_scales; ///< fp8 only
-  const float *down_scales;    ///< fp8 only
+  const float *up_gate_scales; ///< e4m3: f32 block scales; MXFP4: E8M0 bytes
+  const float *down_scales;    ///< e4m3: f32 block scales; MXFP4: E8M0 bytes
   const float *router_bias;    ///< [experts] added to the scores before rounding, or null
   void *out;                   ///< [tokens, hidden_size] bf16
   void *workspace;             ///< uniserve_moe_layer_workspace() bytes, 256-byte aligned
@@ -33,7 +37,7 @@ struct uniserve_moe_layer_call {
   int64_t top;
   int64_t intermediate;
   int64_t renormalize;
-  int64_t weight_dtype;        ///< UNISERVE_DTYPE_BF16 or UNISERVE_DTYPE_F8E4M3
+  int64_t weight_dtype;        ///< UNISERVE_DTYPE_BF16, _F8E4M3 or _F4E2M1
   int64_t multiprocessors;
   char error[512];
 };
@@ -58,10 +62,11 @@ struct uniserve_moe_layer_views {
   int64_t num_non_exiting_tiles;///< [1] i32
   int64_t gated;               ///< [permuted_rows, intermediate] bf16
   int64_t products;            ///< [permuted_rows, hidden_size] bf16
-  int64_t hidden_q;            ///< fp8: [tokens, hidden_size] e4m3
-  int64_t hidden_s;            ///< fp8: [tokens, hidden_size / 128] f32
+  int64_t hidden_q;            ///< fp8 and MX: [tokens, hidden_size] e4m3
+  int64_t hidden_s;            ///< fp8: [tokens, hidden_size / 128] f32; MX: [tokens, hidden_size / 32] E8M0
   int64_t gated_q;             ///< fp8: [permuted_rows, intermediate] e4m3
-  int64_t gated_s;             ///< fp8: [permuted_rows, intermediate / 128] f32, or with
+  int64_t gated_s;             ///< MX: [permuted_rows, intermediate / 32] E8M0;
+                               ///< fp8: [permuted_rows, intermediate / 128] f32, or with
                                ///< route_scales [intermediate / 128, permuted_rows]
   int64_t hidden_route_s;      ///< fp8 with route_scales: [hidden_size / 128, permuted_rows] f32,
                                ///< the scale of each route's token by permuted row; else -1
@@ -79,7 +84,7 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_views_of(int64_t tokens, int64_t hi
 
 UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_call *call, void *stream);
 
-/// The layer's launches in order; the e4m3 steps launch nothing for bf16 weights, and
+/// The layer's launches in order; the quantiser steps launch nothing for bf16 weights, and
 /// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised.
 enum uniserve_moe_layer_step {
   UNISERVE_MOE_LAYER_ROUTER = 0,

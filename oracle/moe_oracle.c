@@ -726,6 +726,7 @@ uint8_t oracle_mx_scale(float amax, float limit) {
   frexpf(amax / limit, &e);                      /* amax / limit in [2^(e-1), 2^e) */
   while (e > -127 && amax <= ldexpf(limit, e - 1)) --e;
   while (e < 127 && amax > ldexpf(limit, e)) ++e;
+  if (e < -127) e = -127;                        /* a subnormal block: 2^-127 already holds it */
   return (uint8_t)(e + 127);
 }
 

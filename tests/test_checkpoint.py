@@ -22,7 +22,8 @@ import pytest
 import torch
 from safetensors.torch import load_file
 
-from uniserve_moe.checkpoint import ExpertNames, quantize_blocks_e4m3, router_weight, slot_map, stack_experts
+from uniserve_moe.checkpoint import (ExpertNames, quantize_blocks_e4m3, quantize_blocks_mxfp4, router_weight, slot_map,
+                                    stack_experts)
 
 FIXTURE = Path(__file__).resolve().parent / "golden" / "qwen3_moe"
 UNIT_ROUNDOFF = np.float32(np.finfo(np.float32).eps / 2)
@@ -97,6 +98,25 @@ def test_block_quantiser_matches_the_oracle(oracle):
     want_codes, want_scales = oracle.quantize_blocks_fp8(w.view(torch.int16).numpy().view(np.uint16))
     np.testing.assert_array_equal(codes.numpy(), want_codes)
     np.testing.assert_array_equal(scales.numpy().view(np.uint32), want_scales.view(np.uint32))
+
+
+def test_mxfp4_quantiser_matches_the_oracle(oracle):
+    """The host-side MXFP4 quantiser writes the oracle's pairs and E8M0 bytes bit for bit, over
+    every rounding tie, signed zeros, an all-zero block, an outlier and blocks whose exponent
+    clamps at -127."""
+    rng = np.random.default_rng(8)
+    w = torch.from_numpy(rng.normal(0.0, 0.02, (3, 64, 256)).astype(np.float32)).to(torch.bfloat16)
+    w[0, 0, :32] = 0.0
+    ties = [6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -0.1, -5.0, 4.5, 0.5, 2.75]
+    w[0, 1, 32:32 + len(ties)] = torch.tensor(ties)
+    w[1, 2, 64:96] = 0.0
+    w[1, 2, 70] = -1.0e-38                                   # subnormal amax: exponent clamps at -127
+    w[2, 3, 5] = 3.0e4
+    pairs, scales = quantize_blocks_mxfp4(w)
+    want_pairs, want_scales = oracle.quantize_blocks_mxfp4(w.view(torch.int16).numpy().view(np.uint16))
+    np.testing.assert_array_equal(scales.numpy(), want_scales)
+    np.testing.assert_array_equal(pairs.numpy(), want_pairs)
+    assert scales[0, 0, 0] == 127 and scales[0, 1, 1] == 127
 
 
 # ---- the tiny model ----------------------------------------------------------------------------

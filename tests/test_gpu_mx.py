@@ -25,6 +25,7 @@ def test_mxfp8_quantiser_is_bit_exact(device):
     x = (rng.standard_normal((300, 512)) * np.exp(rng.normal(0, 4, (300, 1)))).astype(np.float32)
     x[3, :64] = 0.0
     x[7, 5] = 3.0e38
+    x[9, 32:64] = 1.0e-39                                 # subnormal block: exponent clamps at -127
     bits = O.bf16_encode(x)
     t = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(device)
     q, s = ops.quantize_mxfp8(t)
@@ -85,3 +86,108 @@ def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew):
     want_products = O.route_gemm_mx(gq.cpu().numpy()[:padded], gs.cpu().numpy()[:padded], q2, s2, sort)
     got_products = bf16_values(products)
     assert_bf16_bar(got_products[:padded][live], want_products[:padded][live], "route_gemm_mx", max_rel=1e-2)
+
+
+MX_LAYERS = {
+    # name: tokens, hidden, experts, top, intermediate, zipf, oracle sample
+    "30b decode mx": (64, 2048, 128, 8, 768, False, None),
+    "30b prefill mx zipf": (8192, 2048, 128, 8, 768, True, 96),
+    "235b decode mx one token": (1, 4096, 128, 8, 1536, False, None),
+}
+
+
+def mx_layer_inputs(device, tokens, hidden, experts, intermediate, seed=0):
+    x = normal_bf16((tokens, hidden), seed + 1, device=device)
+    router = normal_bf16((experts, hidden), seed + 2, 0.02, device)
+    q1, s1, q2, s2 = mx_stacks(device, experts, hidden, intermediate, seed + 3)
+    return x, router, (q1, s1, q2, s2)
+
+
+def on(device, host):
+    return [torch.from_numpy(a).to(device) for a in host]
+
+
+@pytest.mark.parametrize("case", list(MX_LAYERS))
+def test_mx_layer_against_the_oracle(device, case):
+    """The whole layer over MXFP4 stacks against the oracle's composition: router ids bit-exact;
+    outputs within 4e-2 of the peak (the gated rows are re-quantised to MXFP8 on both sides from
+    bf16 values that may differ in their last bit, which moves a code by one step)."""
+    tokens, hidden, experts, top, intermediate, zipf, sample = MX_LAYERS[case]
+    announce("mx layer", case)
+    x, router, host_w = mx_layer_inputs(device, tokens, hidden, experts, intermediate)
+    w1, s1, w2, s2 = on(device, host_w)
+    bias = torch.from_numpy(zipf_bias(experts)).to(device) if zipf else None
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f4e2m1")
+    out = layer(x, router, w1, w2, up_gate_scales=s1, down_scales=s2, router_bias=bias)
+    torch.cuda.synchronize()
+    ids = layer.view("ids", torch.int32, (tokens, top)).cpu().numpy()
+    got = bf16_values(out)
+    assert np.isfinite(got).all()
+    rows = np.arange(tokens) if sample is None else np.random.default_rng(0).choice(tokens, sample, replace=False)
+    x_bits = bf16_bits(x)[rows]
+    if zipf:
+        scores = layer.view("scores", torch.bfloat16, (tokens, experts))
+        want_ids, _ = O.topk_softmax(bf16_bits(scores)[rows], top, score_kind=1)
+        np.testing.assert_array_equal(ids[rows], want_ids)
+        weights = layer.view("weights", torch.float32, (tokens, top)).cpu().numpy()[rows]
+        want = sampled_mx_layer(x_bits, ids[rows], weights, host_w, experts, top)
+    else:
+        want_bits, want_ids, _, _ = O.moe_layer(x_bits, bf16_bits(router), host_w[0], host_w[2], top,
+                                                up_gate_scales=host_w[1], down_scales=host_w[3])
+        np.testing.assert_array_equal(ids[rows], want_ids)
+        want = O.bf16_decode(want_bits).astype(np.float64)
+    assert_bf16_bar(got[rows], want, case, max_rel=4e-2)
+
+
+def sampled_mx_layer(x_bits, ids, weights, host_w, experts, top):
+    """The oracle's MX products and combine for a sample of tokens with given routes."""
+    tokens = x_bits.shape[0]
+    w1, s1, w2, s2 = host_w
+    sort = O.moe_sort(ids, experts)
+    rows = O.max_tiles(tokens, top, experts) * 128
+    xq, xs = O.quantize_rows_mxfp8(x_bits)
+    gated = O.gather_gemm_mx(xq, xs, w1, s1, top, sort, rows, fill=0.0)
+    gq, gs = O.quantize_rows_mxfp8(O.bf16_encode(gated))
+    products = O.route_gemm_mx(gq, gs, w2, s2, sort, fill=0.0)
+    combined = O.moe_unpermute(O.bf16_encode(products),
+                               sort["expanded_to_permuted"][: tokens * top].reshape(tokens, top), weights)
+    return O.bf16_decode(O.bf16_encode(combined)).astype(np.float64)
+
+
+def test_mx_layer_graph_replays_match_eager(device):
+    announce("mx layer graph")
+    tokens, hidden, experts, top, intermediate = 64, 2048, 128, 8, 768
+    x, router, host_w = mx_layer_inputs(device, tokens, hidden, experts, intermediate, 20)
+    w1, s1, w2, s2 = on(device, host_w)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f4e2m1")
+    out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=device)
+    layer(x, router, w1, w2, out=out, up_gate_scales=s1, down_scales=s2)
+    torch.cuda.synchronize()
+    eager = bf16_bits(out).copy()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            layer(x, router, w1, w2, out=out, up_gate_scales=s1, down_scales=s2)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        out.zero_()
+        _ = torch.randn(1000, device=device).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bf16_bits(out), eager, err_msg=f"replay {replay}")
+
+
+def test_device_mxfp4_quantiser_matches_the_oracle(device):
+    """The package's stack quantiser, run on the device, writes the oracle's pairs and scales."""
+    from uniserve_moe.checkpoint import quantize_blocks_mxfp4
+
+    announce("mxfp4 stack quantiser on device")
+    w = normal_bf16((4, 256, 512), 9, 0.02, device)
+    pairs, scales = quantize_blocks_mxfp4(w)
+    torch.cuda.synchronize()
+    want_pairs, want_scales = O.quantize_blocks_mxfp4(bf16_bits(w))
+    np.testing.assert_array_equal(scales.cpu().numpy(), want_scales)
+    np.testing.assert_array_equal(pairs.cpu().numpy(), want_pairs)

@@ -606,6 +606,11 @@ def test_mx_scale_is_the_smallest_power_without_saturation():
             assert amax <= limit * 2.0 ** e, (amax, limit, e)
             assert amax > limit * 2.0 ** (e - 1), (amax, limit, e)
     assert O.mx_scale(0.0, 448.0) == 127 and O.mx_scale(float("inf"), 6.0) == 127
+    # Blocks far below 2^-127: the exponent clamps at the smallest E8M0 power (byte 0), never the
+    # NaN byte, and that power still holds them.
+    for amax in (1.0e-38, 1.0e-40, 2.0 ** -149, 2.0 ** -126):
+        for limit in (6.0, 448.0):
+            assert O.mx_scale(amax, limit) == 0, (amax, limit)
 
 
 def test_mxfp8_rows_match_torch_cast_under_the_scale():

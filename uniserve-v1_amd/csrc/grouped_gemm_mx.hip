@@ -49,6 +49,7 @@ __device__ __forceinline__ uint32_t mx_scale(float amax, float limit) {
   frexpf(amax / limit, &e);
   while (e > -127 && amax <= ldexpf(limit, e - 1)) --e;
   while (e < 127 && amax > ldexpf(limit, e)) ++e;
+  if (e < -127) e = -127;  // a subnormal block: 2^-127 already holds it
   return static_cast<uint32_t>(e + 127);
 }
 

@@ -5,7 +5,8 @@
 // order (the order crates/nn/tests/moe.rs:1402-1438 records); this driver issues the same entries
 // on one stream over intermediates carved from a caller-owned workspace, so it allocates nothing,
 // reads nothing back and can be captured into a HIP graph. With e4m3 weights the activations of
-// each product are quantised per row per 128 channels first (two more launches).
+// each product are quantised per row per 128 channels first (two more launches); with MXFP4
+// weights they are quantised to MXFP8 (per row per 32 channels, E8M0 scales) the same way.
 #include <cstring>
 
 #include "common.hpp"
@@ -14,6 +15,7 @@
 #include "uniserve_gather_gemm.h"
 #include "uniserve_moe_fp8.h"
 #include "uniserve_moe_layer.h"
+#include "uniserve_moe_mx.h"
 #include "uniserve_moe_sort.h"
 #include "uniserve_moe_unpermute.h"
 #include "uniserve_route_gemm.h"
@@ -29,7 +31,9 @@ int64_t aligned(int64_t bytes) { return (bytes + kAlign - 1) / kAlign * kAlign; 
 bool views_of(int64_t tokens, int64_t hidden, int64_t experts, int64_t top, int64_t intermediate,
               int64_t weight_dtype, uniserve_moe_layer_views *v) {
   if (tokens < 0 || hidden <= 0 || experts <= 0 || top <= 0 || top > experts || intermediate <= 0) return false;
-  if (weight_dtype != UNISERVE_DTYPE_BF16 && weight_dtype != UNISERVE_DTYPE_F8E4M3) return false;
+  if (weight_dtype != UNISERVE_DTYPE_BF16 && weight_dtype != UNISERVE_DTYPE_F8E4M3 &&
+      weight_dtype != UNISERVE_DTYPE_F4E2M1)
+    return false;
   std::memset(v, 0, sizeof(*v));
   v->max_tiles = uniserve_moe_max_tiles(tokens, top, experts, kTile);
   v->permuted_rows = v->max_tiles * kTile;
@@ -58,6 +62,12 @@ bool views_of(int64_t tokens, int64_t hidden, int64_t experts, int64_t top, int6
     v->gated_s = take(v->permuted_rows * (intermediate / 128) * 4);
     v->route_scales = uniserve::fp8_route_scales(tokens, top, experts, hidden, intermediate, v->permuted_rows) ? 1 : 0;
     v->hidden_route_s = v->route_scales ? take(v->permuted_rows * (hidden / 128) * 4) : -1;
+  } else if (weight_dtype == UNISERVE_DTYPE_F4E2M1) {
+    v->hidden_q = take(tokens * hidden);
+    v->hidden_s = take(tokens * (hidden / 32));
+    v->gated_q = take(v->permuted_rows * intermediate);
+    v->gated_s = take(v->permuted_rows * (intermediate / 32));
+    v->hidden_route_s = -1;
   } else {
     v->hidden_q = v->hidden_s = v->gated_q = v->gated_s = v->hidden_route_s = -1;
   }
@@ -94,6 +104,80 @@ extern "C" int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_s
 
 namespace {
 
+/// MXFP4 experts: quantise the hidden rows to MXFP8, FC1, quantise the live gated rows, FC2.
+template <class Want>
+int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_layer_views &v, char *ws,
+                        const Want &want, void *stream) {
+  auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
+  const auto *t2e = static_cast<const int32_t *>(at(v.tile_to_expert));
+  const auto *t2l = static_cast<const int32_t *>(at(v.tile_to_limit));
+  const auto *p2e = static_cast<const int32_t *>(at(v.permuted_to_expanded));
+  const auto *tiles = static_cast<const int32_t *>(at(v.num_non_exiting_tiles));
+
+  uniserve_quantize_mxfp8_call qx{};
+  qx.input = call->hidden;
+  qx.out = at(v.hidden_q);
+  qx.scales = static_cast<uint8_t *>(at(v.hidden_s));
+  qx.rows = call->tokens;
+  qx.width = call->hidden_size;
+  qx.input_dtype = UNISERVE_DTYPE_BF16;
+  if (want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) && uniserve_quantize_mxfp8(&qx, stream) != 0)
+    return forward_error(call, "quantize_mxfp8", qx);
+
+  // The call's scale pointers carry E8M0 bytes for MXFP4 stacks.
+  uniserve_gather_mx_call fc1{};
+  fc1.hidden = at(v.hidden_q);
+  fc1.hidden_scales = static_cast<const uint8_t *>(at(v.hidden_s));
+  fc1.weights = call->up_gate;
+  fc1.weight_scales = reinterpret_cast<const uint8_t *>(call->up_gate_scales);
+  fc1.out = at(v.gated);
+  fc1.tile_to_expert = t2e;
+  fc1.tile_to_limit = t2l;
+  fc1.permuted_to_expanded = p2e;
+  fc1.num_non_exiting_tiles = tiles;
+  fc1.tokens = call->tokens;
+  fc1.permuted_rows = v.permuted_rows;
+  fc1.width = 2 * call->intermediate;
+  fc1.hidden_size = call->hidden_size;
+  fc1.experts = call->experts;
+  fc1.top = call->top;
+  fc1.out_dtype = UNISERVE_DTYPE_BF16;
+  fc1.multiprocessors = call->multiprocessors;
+  if (want(UNISERVE_MOE_LAYER_GATHER) && uniserve_gather_gemm_mx(&fc1, stream) != 0)
+    return forward_error(call, "gather_gemm_mx", fc1);
+
+  uniserve_quantize_mxfp8_call qg{};
+  qg.input = at(v.gated);
+  qg.out = at(v.gated_q);
+  qg.scales = static_cast<uint8_t *>(at(v.gated_s));
+  qg.row_limit = static_cast<const int32_t *>(at(v.total_padded_tokens));
+  qg.rows = v.permuted_rows;
+  qg.width = call->intermediate;
+  qg.input_dtype = UNISERVE_DTYPE_BF16;
+  if (want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) && uniserve_quantize_mxfp8(&qg, stream) != 0)
+    return forward_error(call, "quantize_mxfp8", qg);
+
+  uniserve_route_mx_call fc2{};
+  fc2.rows = at(v.gated_q);
+  fc2.row_scales = static_cast<const uint8_t *>(at(v.gated_s));
+  fc2.weights = call->down;
+  fc2.weight_scales = reinterpret_cast<const uint8_t *>(call->down_scales);
+  fc2.out = at(v.products);
+  fc2.tile_to_expert = t2e;
+  fc2.tile_to_limit = t2l;
+  fc2.permuted_to_expanded = p2e;
+  fc2.num_non_exiting_tiles = tiles;
+  fc2.permuted_rows = v.permuted_rows;
+  fc2.width = call->hidden_size;
+  fc2.intermediate = call->intermediate;
+  fc2.experts = call->experts;
+  fc2.out_dtype = UNISERVE_DTYPE_BF16;
+  fc2.multiprocessors = call->multiprocessors;
+  if (want(UNISERVE_MOE_LAYER_ROUTE) && uniserve_route_gemm_mx(&fc2, stream) != 0)
+    return forward_error(call, "route_gemm_mx", fc2);
+  return 0;
+}
+
 /// The layer's launches, all of them (`only` < 0) or the one step `only`.
 int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *stream) {
   using namespace uniserve;
@@ -103,8 +187,11 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         call->down == nullptr || call->out == nullptr || call->workspace == nullptr)
       return UNISERVE_REFUSE(call, "moe_layer needs hidden, router, both stacks, out and a workspace");
     const bool fp8 = call->weight_dtype == UNISERVE_DTYPE_F8E4M3;
-    if (fp8 && (call->up_gate_scales == nullptr || call->down_scales == nullptr))
-      return UNISERVE_REFUSE(call, "moe_layer: e4m3 stacks need their block scales");
+    const bool mx = call->weight_dtype == UNISERVE_DTYPE_F4E2M1;
+    if ((fp8 || mx) && (call->up_gate_scales == nullptr || call->down_scales == nullptr))
+      return UNISERVE_REFUSE(call, "moe_layer: quantised stacks need their block scales");
+    if (mx && (call->hidden_size % 256 != 0 || call->intermediate % 256 != 0))
+      return UNISERVE_REFUSE(call, "moe_layer: MXFP4 stacks need hidden and intermediate sizes of whole 256-element chunks");
     if (reinterpret_cast<uintptr_t>(call->workspace) % kAlign != 0)
       return UNISERVE_REFUSE(call, "moe_layer needs a 256-byte aligned workspace");
     uniserve_moe_layer_views v;
@@ -170,7 +257,9 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (want(UNISERVE_MOE_LAYER_SORT) && uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
 
     // 4-5. The two products.
-    if (!fp8) {
+    if (mx) {
+      if (int32_t status = run_mx_products(call, v, ws, want, stream)) return status;
+    } else if (!fp8) {
       uniserve_gather_call fc1{};
       fc1.hidden = call->hidden;
       fc1.weights = call->up_gate;

@@ -131,3 +131,33 @@ def quantize_blocks_e4m3(stack, block=128):
     codes = (blocks / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
     return (codes.reshape(stacks, n, k).view(torch.uint8).contiguous(),
             scale.reshape(stacks, n // block, k // block).contiguous())
+
+
+def quantize_blocks_mxfp4(stack):
+    """OCP MXFP4 form of a ``[stacks, N, K]`` stack: one E8M0 scale byte per 32 consecutive K
+    elements, the smallest power of two 2^e with ``blockmax <= 6 * 2^e`` (2^0 for an all-zero
+    block, e clamped to [-127, 127]), and E2M1 codes of ``w / 2^e`` rounded to nearest, ties to
+    the even code, saturating at 6; two codes per byte, the lower K index in the low nibble.
+    Returns ``(pairs uint8 [stacks, N, K/2], scales uint8 [stacks, N, K/32])``.
+    """
+    stacks, n, k = stack.shape
+    if k % 32:
+        raise ValueError("the stack's K extent is not whole 32-element blocks")
+    blocks = stack.float().reshape(stacks, n, k // 32, 32)
+    amax = blocks.abs().amax(dim=3, keepdim=True)
+    live = (amax > 0) & torch.isfinite(amax)
+    safe = torch.where(live, amax, torch.ones_like(amax))
+    e = torch.frexp(safe / 6.0).exponent.to(torch.int32)
+    # amax / 6 rounds; settle the exponent on exact power-of-two comparisons.
+    e = torch.where(safe <= torch.ldexp(torch.full_like(safe, 6.0), (e - 1).float()), e - 1, e)
+    e = torch.where(safe > torch.ldexp(torch.full_like(safe, 6.0), e.float()), e + 1, e)
+    e = torch.where(live, e.clamp(-127, 127), torch.zeros_like(e))
+    scaled = blocks / torch.ldexp(torch.ones_like(safe), e.float())
+    a = scaled.abs()
+    # Midpoints between neighbouring magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6; a tie takes the even code.
+    code = ((a > 0.25).int() + (a >= 0.75).int() + (a > 1.25).int() + (a >= 1.75).int() + (a > 2.5).int() +
+            (a >= 3.5).int() + (a > 5.0).int())
+    code = torch.where(torch.isnan(scaled), torch.zeros_like(code), code | (torch.signbit(scaled).int() << 3))
+    code = code.to(torch.uint8).reshape(stacks, n, k // 2, 2)
+    pairs = code[..., 0] | (code[..., 1] << 4)
+    return pairs.contiguous(), (e + 127).to(torch.uint8).reshape(stacks, n, k // 32).contiguous()
