@@ -6,6 +6,9 @@ the hardware's block scaling is exact (powers of two) and the FP32 sums differ o
 the gap is the bf16 rounding of the outputs: max |got - want| <= 1e-2 of the peak (and the mean
 within BASELINE's 1e-3). Parity unpinned against the reference: it has no MX operator (its four-bit
 experts are NVFP4).
+
+Decode-shaped cases (few routes per expert) run the stream kernel; the 512- and 1024-token Zipf
+cases and the 8192-token layer run the tiled prefill kernel for both products.
 """
 
 import numpy as np
@@ -51,7 +54,8 @@ def mx_stacks(device, experts, hidden, intermediate, seed=2):
 
 
 @pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew", [
-    (64, 2048, 128, 8, 768, "uniform"), (1, 4096, 128, 8, 1536, "uniform"), (512, 2048, 128, 8, 768, "zipf")])
+    (64, 2048, 128, 8, 768, "uniform"), (1, 4096, 128, 8, 1536, "uniform"), (512, 2048, 128, 8, 768, "zipf"),
+    (1024, 4096, 128, 8, 1536, "zipf")])
 def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew):
     announce("mx products", tokens, hidden, experts, top, intermediate, skew)
     rng = np.random.default_rng(tokens + 7)

@@ -14,12 +14,15 @@
 // So the hardware applies both MX block scales itself and the products accumulate straight into
 // the FP32 accumulator: no per-block scaling on the VALU.
 //
-// The product kernel is the decode-shaped stream kernel of the e4m3 products (one tile x a slice of
-// weight rows per workgroup; weights streamed as whole 128-byte lines, non-temporal, and regrouped
-// into the MFMA layout with ds_bpermute), walking K 256 elements (one 128-byte weight line) at a
-// time; at prefill shapes it takes each tile in passes of 16 tokens.
+// Two product kernels, chosen by routes per expert as for the e4m3 products:
+//  * decode shapes: the stream kernel (one tile x a slice of weight rows per workgroup; weights
+//    streamed as whole 128-byte lines, non-temporal, and regrouped into the MFMA layout with
+//    ds_bpermute), walking K 256 elements (one 128-byte weight line) at a time;
+//  * prefill shapes: the tiled kernel (one 128-row tile x 512 weight rows per workgroup), both
+//    operands and both scale tables staged through LDS by DMA in three stages of 128 K.
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "grouped_prefill.hpp"
 #include "uniserve_moe_mx.h"
 
 namespace uniserve {
@@ -305,6 +308,238 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   }
 }
 
+// ---- the tiled (prefill) kernel ---------------------------------------------------------------------------
+//
+// One workgroup of 8 wavefronts (two per SIMD) owns one 128-row sort tile and 512 weight rows of its
+// expert (FC1: 256 up rows and the matching 256 gate rows; FC2: 512 output columns). Wave w owns
+// weight rows 64 w .. 64 w + 63 of the slice (FC1: 32 up rows then the 32 gate rows of the same
+// columns) as four 16-row blocks, times all 128 tile rows as eight 16-row blocks: 32 MFMAs of
+// 16x16x128 per 128-K stage, 32 accumulators of four floats.
+//
+// A stage holds, per row, 128 e4m3 activation bytes (8 chunks of 16), 64 bytes of E2M1 weight pairs
+// (4 chunks) and one 4-byte word of E8M0 scales for each of the two operands (the stage's four
+// 32-element blocks). Every byte arrives by DMA (`global_load_lds_dword[x4]`), eight instructions per
+// wave per stage, so the loop counts its loads exactly: three stages in flight, stage k + 2 issued
+// while stage k multiplies, one barrier per stage. Chunk c of a row sits at c ^ key(row) (activation
+// rows: key (r >> 1) & 7; weight rows: key (r >> 2) & 3), so the 16 rows one MFMA fragment read
+// touches hit all 64 banks once. The activation-scale words are loaded by all 64 lanes of every wave
+// (lanes 16.. repeat the wave's 16 rows), so each wave has one such instruction per stage.
+
+constexpr int kTiledWaves = 8;
+constexpr int kTiledThreads = kTiledWaves * kWave;
+constexpr int kTiledStages = 3;
+constexpr int kSliceRows = kTiledWaves * 64;          // weight rows per workgroup
+constexpr int kTiledLoads = 8;                        // DMA instructions per wave per stage
+
+struct MxTiledParams {
+  MxParams base;
+  int32_t slices;          ///< weight-row slices per tile
+  int32_t max_tiles;
+  int32_t group;           ///< tiles per group of the numbering
+  int32_t groups_per_xcd;
+};
+
+struct MxStage {
+  u32x4 act[kTileRows * 8];        // 16 KB
+  u32x4 weights[kSliceRows * 4];   // 32 KB
+  uint32_t weight_scales[kSliceRows];
+  uint32_t act_scales[kTiledWaves * kWave];  // wave w's rows 16 w + (l & 15) at 64 w + l
+};
+
+__device__ __forceinline__ int act_slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+__device__ __forceinline__ int weight_slot(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 2) & 3)); }
+
+/// One 4-byte DMA per lane from `base` + `offset` into LDS at `lds` + 4 * lane (see `dma16`).
+__device__ __forceinline__ void dma4(const void *base, uint32_t offset, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %0, %1\n\t"
+      :
+      : "v"(offset), "s"(base), "s"(lds)
+      : "m0");
+}
+
+template <bool kGated>
+__global__ void __launch_bounds__(kTiledThreads) tiled_mx_kernel(MxTiledParams tp) {
+  using prefill::dma16;
+  using prefill::lds_address;
+  const MxParams &p = tp.base;
+  __shared__ MxStage ring[kTiledStages];
+
+  // ---- the work item: groups of `group` tiles, slice-major inside a group, dealt to the XCDs in
+  // turn (block b runs on XCD b % 8) ----
+  const int b = static_cast<int>(blockIdx.x);
+  const int span = tp.group * tp.slices;
+  const int seq = b >> 3;
+  const int group_index = (seq / span) * 8 + (b & 7);
+  const int first_tile = group_index * tp.group;
+  if (first_tile >= tp.max_tiles) return;
+  const int in_group = min(tp.group, tp.max_tiles - first_tile);
+  const int within = seq - (seq / span) * span;
+  if (within >= in_group * tp.slices) return;
+  const int slice = within / in_group;
+  const int tile = first_tile + within % in_group;
+  if (tile >= p.num_tiles[0]) return;
+
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int t = static_cast<int>(threadIdx.x);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int stages = static_cast<int>(p.K / 128);
+  const int64_t weight_row_bytes = p.K / 2;
+  const int64_t scale_row_bytes = p.K / 32;
+  const int top = static_cast<int>(p.top);
+  // The activation row behind tile row r (FC1 gathers tokens; padding rows read row 0 or the
+  // tile's first row).
+  auto source_row = [&](int r) -> int64_t {
+    if constexpr (kGated) {
+      const int expanded = p.permuted_to_expanded[first + r];
+      return r < rows ? static_cast<int64_t>(expanded / top) : 0;
+    } else {
+      return r < rows ? first + r : first;
+    }
+  };
+
+  // ---- DMA sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
+  // Activations: instruction i fills rows 8 (2 w + i) + l / 8, lane l bringing logical chunk
+  // (l % 8) ^ key(row) into physical chunk l % 8.
+  uint32_t a_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (2 * wave + i) * 8 + lane / 8;
+    a_off[i] = static_cast<uint32_t>(source_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
+  }
+  const uint32_t as_off = static_cast<uint32_t>(source_row(16 * wave + r16) * scale_row_bytes);
+  // Weights: the wave's local row j (0..63) is, for FC1, up row col + j (j < 32) or gate row
+  // out_width + col + j - 32; for FC2, row col + j. Instruction i fills local rows 16 i + l / 4,
+  // lane l bringing logical chunk (l % 4) ^ key into physical chunk l % 4, key = (l / 16) % 4.
+  const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSliceRows / 2 : kSliceRows);
+  const int64_t wave_col = slice_col + wave * (kGated ? 32 : 64);
+  auto weight_row = [&](int j) -> int64_t {
+    if constexpr (kGated) return j < 32 ? wave_col + j : p.out_width + wave_col + j - 32;
+    else return wave_col + j;
+  };
+  const uint8_t *expert_weights = p.weights + expert * p.n_total * weight_row_bytes;
+  const uint32_t w_off = static_cast<uint32_t>((lane / 4) * weight_row_bytes + ((lane & 3) ^ ((lane >> 4) & 3)) * 16);
+  const uint8_t *expert_scales = p.weight_scales + expert * p.n_total * scale_row_bytes;
+  const uint32_t ws_off = static_cast<uint32_t>(weight_row(lane) * scale_row_bytes);
+
+  auto issue = [&](MxStage &st, int k) {
+    const uint32_t act_lds = lds_address(st.act + wave * 2 * kWave);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+    const uint32_t weight_lds = lds_address(st.weights + wave * 64 * 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(expert_weights + weight_row(16 * i) * weight_row_bytes + static_cast<int64_t>(k) * 64, w_off,
+            __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
+    dma4(expert_scales + static_cast<int64_t>(k) * 4, ws_off,
+                 __builtin_amdgcn_readfirstlane(lds_address(st.weight_scales + wave * 64)));
+    dma4(p.act_scales + static_cast<int64_t>(k) * 4, as_off,
+                 __builtin_amdgcn_readfirstlane(lds_address(st.act_scales + wave * kWave)));
+  };
+
+  floatx4 acc[8][4];
+#pragma unroll
+  for (int tb = 0; tb < 8; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](const MxStage &st) {
+    u32x4 wf[4];
+    uint32_t sw[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const int row = wave * 64 + jb * 16 + r16;
+      wf[jb] = st.weights[weight_slot(row, g)];
+      sw[jb] = reinterpret_cast<const uint8_t *>(st.weight_scales)[row * 4 + g];
+    }
+#pragma unroll
+    for (int tb = 0; tb < 8; ++tb) {
+      const int row = tb * 16 + r16;
+      const u32x4 lo = st.act[act_slot(row, g)];
+      const u32x4 hi = st.act[act_slot(row, g + 4)];
+      const intx8 x = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                            static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+      const uint32_t sx = reinterpret_cast<const uint8_t *>(st.act_scales)[(tb * kWave + r16) * 4 + g];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = mfma_mx(wf[jb], x, sw[jb], sx, acc[tb][jb]);
+    }
+  };
+
+  // ---- the K loop: at the top of stage k, stages k and k + 1 are in flight; wait for k (loads
+  // land in issue order), then the barrier: every wave's stage k has landed and every wave is done
+  // with stage k - 1, whose buffer takes stage k + 2. Issues past the last stage re-read it, so
+  // every wait counts the same loads. ----
+  issue(ring[0], 0);
+  issue(ring[1], min(1, stages - 1));
+  for (int k = 0; k < stages; ++k) {
+    prefill::wait_loads_but<kTiledLoads>();
+    __syncthreads();
+    issue(ring[(k + 2) % kTiledStages], min(k + 2, stages - 1));
+    compute(ring[k % kTiledStages]);
+  }
+  prefill::wait_all_loads();
+  __syncthreads();  // every wave is done reading the stage buffers
+
+  // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, token row 16 tb + r16
+  // and the wave's weight rows 16 jb + 4 g + i in element i. The output tile goes through LDS so
+  // the global stores are whole rows; LDS rows are padded by 32 bytes. ----
+  constexpr int kOutCols = kGated ? kSliceRows / 2 : kSliceRows;
+  constexpr int kOutStride = kOutCols * 2 + 32;
+  static_assert(kTileRows * kOutStride <= static_cast<int>(sizeof(ring)), "the output tile fits the stages");
+  char *tile_lds = reinterpret_cast<char *>(ring);
+#pragma unroll
+  for (int tb = 0; tb < 8; ++tb) {
+    char *row = tile_lds + (tb * 16 + r16) * kOutStride;
+    if constexpr (kGated) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        floatx4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + 2][i]) * acc[tb][jb][i];
+        store_bf16x4(reinterpret_cast<uint16_t *>(row + (wave * 32 + jb * 16 + 4 * g) * 2), v);
+      }
+    } else {
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+        store_bf16x4(reinterpret_cast<uint16_t *>(row + (wave * 64 + jb * 16 + 4 * g) * 2), acc[tb][jb]);
+    }
+  }
+  __syncthreads();
+  constexpr int kPieces = kOutCols / 8;
+  for (int index = t; index < kTileRows * kPieces; index += kTiledThreads) {
+    const int m = index / kPieces;
+    const int c = index - m * kPieces;
+    if (m >= rows) continue;
+    const u32x4 piece = *reinterpret_cast<const u32x4 *>(tile_lds + m * kOutStride + c * 16);
+    *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
+  }
+}
+
+/// Whether the tiled kernel serves the shape: whole 128-K stages and whole 512-row weight slices.
+bool tiled_fits(bool gated, int64_t K, int64_t out_width) {
+  return K % 128 == 0 && K > 0 && out_width % (gated ? kSliceRows / 2 : kSliceRows) == 0;
+}
+
+void launch_tiled_mx(const MxParams &p, bool gated, int64_t max_tiles, hipStream_t stream) {
+  MxTiledParams tp{};
+  tp.base = p;
+  tp.slices = static_cast<int32_t>(p.out_width / (gated ? kSliceRows / 2 : kSliceRows));
+  tp.max_tiles = static_cast<int32_t>(max_tiles);
+  tp.group = 16;
+  tp.groups_per_xcd = static_cast<int32_t>(ceil_div<int64_t>(ceil_div<int64_t>(max_tiles, tp.group), 8));
+  const int64_t blocks = static_cast<int64_t>(tp.groups_per_xcd) * tp.group * tp.slices * 8;
+  if (gated) hipLaunchKernelGGL((tiled_mx_kernel<true>), dim3(static_cast<uint32_t>(blocks)), dim3(kTiledThreads), 0, stream, tp);
+  else hipLaunchKernelGGL((tiled_mx_kernel<false>), dim3(static_cast<uint32_t>(blocks)), dim3(kTiledThreads), 0, stream, tp);
+}
+
 void launch_mx(const MxParams &p, bool gated, int64_t max_tiles, hipStream_t stream) {
   const int64_t slices = gated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
   if (max_tiles * slices < kSplitBelow) {
@@ -383,7 +618,10 @@ extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, 
     p.n_total = call->width;
     p.out_width = call->width / 2;
     p.top = call->top;
-    launch_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
+    if (!fp8_stream_path(call->tokens * call->top, call->experts) && tiled_fits(true, p.K, p.out_width))
+      launch_tiled_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
+    else
+      launch_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
     return launched(call, "gather_gemm_mx");
   });
 }
@@ -422,7 +660,12 @@ extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, vo
     p.n_total = call->width;
     p.out_width = call->width;
     p.top = 1;
-    launch_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
+    // No token count in the call: the permuted rows less one partial tile per expert bound the routes.
+    const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
+    if (!fp8_stream_path(routes_bound, call->experts) && tiled_fits(false, p.K, p.out_width))
+      launch_tiled_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
+    else
+      launch_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
     return launched(call, "route_gemm_mx");
   });
 }
