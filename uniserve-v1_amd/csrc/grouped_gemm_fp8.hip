@@ -9,10 +9,13 @@
 // activation row. One gfx950 MFMA 16x16x128 (f8f6f4, e4m3 x e4m3) spans exactly one scale block
 // along K, so each block's product is formed exactly as the hardware accumulates it and then added
 // into the FP32 accumulator times s_w * s_x - the per-block dequantisation never touches the
-// operands. The kernels mirror the bf16 ones (`stream` for decode, `tiled` for prefill); the
-// quantiser's codes are bit-exact with the host rule (nearest even, saturating at 448).
+// operands. Decode shapes run the `stream` kernel; prefill shapes run the two-workgroups-per-CU
+// kernel of grouped_dual.hpp, or, where FC1 writes its rows already quantised for FC2, the
+// one-workgroup-per-CU kernel of grouped_prefill.hpp; the quantiser's codes are bit-exact with the
+// host rule (nearest even, saturating at 448).
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "grouped_dual.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_moe_fp8.h"
 
@@ -467,6 +470,10 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
     q.scale_rows = p.scale_rows;
+    if (q.out_codes == nullptr && dual_fits(gated, q.K, q.out_width)) {
+      launch_dual_e4m3(q, gated, max_tiles, stream);
+      return;
+    }
     if (gated) launch_prefill<prefill::E4m3, true>(q, max_tiles, stream);
     else launch_prefill<prefill::E4m3, false>(q, max_tiles, stream);
     return;

@@ -18,8 +18,9 @@
 //  * decode shapes: the stream kernel (one tile x a slice of weight rows per workgroup; weights
 //    streamed as whole 128-byte lines, non-temporal, and regrouped into the MFMA layout with
 //    ds_bpermute), walking K 256 elements (one 128-byte weight line) at a time;
-//  * prefill shapes: the tiled kernel (one 128-row tile x 512 weight rows per workgroup), both
-//    operands and both scale tables staged through LDS by DMA in three stages of 128 K.
+//  * prefill shapes: the tiled kernel (one 128-row tile x 256 weight rows per workgroup, two
+//    workgroups per CU), both operands and both scale tables staged through LDS by DMA in two
+//    stages of 128 K.
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_prefill.hpp"
@@ -310,26 +311,25 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
 
 // ---- the tiled (prefill) kernel ---------------------------------------------------------------------------
 //
-// One workgroup of 8 wavefronts (two per SIMD) owns one 128-row sort tile and 512 weight rows of its
-// expert (FC1: 256 up rows and the matching 256 gate rows; FC2: 512 output columns). Wave w owns
-// weight rows 64 w .. 64 w + 63 of the slice (FC1: 32 up rows then the 32 gate rows of the same
-// columns) as four 16-row blocks, times all 128 tile rows as eight 16-row blocks: 32 MFMAs of
-// 16x16x128 per 128-K stage, 32 accumulators of four floats.
+// One workgroup of 4 wavefronts owns one 128-row sort tile and 256 weight rows of its expert (FC1:
+// 128 up rows and the matching 128 gate rows; FC2: 256 output columns); two workgroups share a CU
+// (two waves per SIMD, one from each), so one workgroup's barrier, DMA wait or epilogue is covered
+// by the other's MFMAs - a single wave issues these scaled MFMAs at only half the peak rate, two
+// interleaved waves at the full rate. Wave (t, w) of the 2 x 2 arrangement multiplies tile rows
+// 64 t .. 64 t + 63 (four 16-row token blocks) by slice rows 128 w .. 128 w + 127 (eight 16-row
+// weight blocks; FC1: 64 up rows then the 64 gate rows of the same columns): 32 MFMAs of 16x16x128
+// per 128-K stage into 32 accumulators of four floats.
 //
 // A stage holds, per row, 128 e4m3 activation bytes (8 chunks of 16), 64 bytes of E2M1 weight pairs
-// (4 chunks) and one 4-byte word of E8M0 scales for each of the two operands (the stage's four
-// 32-element blocks). Every byte arrives by DMA (`global_load_lds_dword[x4]`), eight instructions per
-// wave per stage, so the loop counts its loads exactly: three stages in flight, stage k + 2 issued
-// while stage k multiplies, one barrier per stage. Chunk c of a row sits at c ^ key(row) (activation
-// rows: key (r >> 1) & 7; weight rows: key (r >> 2) & 3), so the 16 rows one MFMA fragment read
-// touches hit all 64 banks once. The activation-scale words are loaded by all 64 lanes of every wave
-// (lanes 16.. repeat the wave's 16 rows), so each wave has one such instruction per stage.
+// (4 chunks) and a 4-byte word of E8M0 scales for each operand (the stage's four 32-element
+// blocks). Every byte arrives by DMA (`global_load_lds_dword[x4]`), ten instructions per wave per
+// stage, so the loop counts its loads exactly: two stages, stage k + 1 issued while stage k
+// multiplies, one barrier per stage. Chunk c of a row sits at c ^ key(row) (activation rows:
+// (r >> 1) & 7; weight rows: (r >> 1) & 3, both measured free of bank conflicts for these reads).
 
-constexpr int kTiledWaves = 8;
+constexpr int kTiledWaves = 4;
 constexpr int kTiledThreads = kTiledWaves * kWave;
-constexpr int kTiledStages = 3;
-constexpr int kSliceRows = kTiledWaves * 64;          // weight rows per workgroup
-constexpr int kTiledLoads = 8;                        // DMA instructions per wave per stage
+constexpr int kSliceRows = 256;                       // weight rows per workgroup
 
 struct MxTiledParams {
   MxParams base;
@@ -341,13 +341,14 @@ struct MxTiledParams {
 
 struct MxStage {
   u32x4 act[kTileRows * 8];        // 16 KB
-  u32x4 weights[kSliceRows * 4];   // 32 KB
+  u32x4 weights[kSliceRows * 4];   // 16 KB
   uint32_t weight_scales[kSliceRows];
-  uint32_t act_scales[kTiledWaves * kWave];  // wave w's rows 16 w + (l & 15) at 64 w + l
+  uint32_t act_scales[kTiledWaves * kWave];  // tile row r at 64 (r / 32) + r % 32
 };
 
 __device__ __forceinline__ int act_slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
-__device__ __forceinline__ int weight_slot(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 2) & 3)); }
+__device__ __forceinline__ int weight_slot(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 1) & 3)); }
+__device__ __forceinline__ int act_scale_slot(int row) { return (row >> 5) * kWave + (row & 31); }
 
 /// One 4-byte DMA per lane from `base` + `offset` into LDS at `lds` + 4 * lane (see `dma16`).
 __device__ __forceinline__ void dma4(const void *base, uint32_t offset, uint32_t lds) {
@@ -361,11 +362,11 @@ __device__ __forceinline__ void dma4(const void *base, uint32_t offset, uint32_t
 }
 
 template <bool kGated>
-__global__ void __launch_bounds__(kTiledThreads) tiled_mx_kernel(MxTiledParams tp) {
+__global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParams tp) {
   using prefill::dma16;
   using prefill::lds_address;
   const MxParams &p = tp.base;
-  __shared__ MxStage ring[kTiledStages];
+  __shared__ MxStage ring[2];
 
   // ---- the work item: groups of `group` tiles, slice-major inside a group, dealt to the XCDs in
   // turn (block b runs on XCD b % 8) ----
@@ -387,6 +388,8 @@ __global__ void __launch_bounds__(kTiledThreads) tiled_mx_kernel(MxTiledParams t
   const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
   const int t = static_cast<int>(threadIdx.x);
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int wt = wave & 1;   // token half
+  const int ww = wave >> 1;  // weight half
   const int lane = lane_id();
   const int r16 = lane & 15;
   const int g = lane >> 4;
@@ -406,110 +409,114 @@ __global__ void __launch_bounds__(kTiledThreads) tiled_mx_kernel(MxTiledParams t
   };
 
   // ---- DMA sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
-  // Activations: instruction i fills rows 8 (2 w + i) + l / 8, lane l bringing logical chunk
-  // (l % 8) ^ key(row) into physical chunk l % 8.
-  uint32_t a_off[2];
+  // Activations: wave w's instruction i fills tile rows 32 w + 8 i + l / 8, lane l bringing logical
+  // chunk (l % 8) ^ key(row) into physical chunk l % 8; its scale instruction brings the scale
+  // words of rows 32 w + l % 32 (lanes 32.. repeat them into the padding).
+  uint32_t a_off[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (2 * wave + i) * 8 + lane / 8;
+  for (int i = 0; i < 4; ++i) {
+    const int r = 32 * wave + 8 * i + lane / 8;
     a_off[i] = static_cast<uint32_t>(source_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
   }
-  const uint32_t as_off = static_cast<uint32_t>(source_row(16 * wave + r16) * scale_row_bytes);
-  // Weights: the wave's local row j (0..63) is, for FC1, up row col + j (j < 32) or gate row
-  // out_width + col + j - 32; for FC2, row col + j. Instruction i fills local rows 16 i + l / 4,
-  // lane l bringing logical chunk (l % 4) ^ key into physical chunk l % 4, key = (l / 16) % 4.
+  const uint32_t as_off = static_cast<uint32_t>(source_row(32 * wave + (lane & 31)) * scale_row_bytes);
+  // Weights: slice row j (0..255) is, for FC1, up row col(j) or gate row out_width + col(j) with
+  // col(j) = slice_col + 64 (j / 128) + j % 64 (up for j % 128 < 64); for FC2, row slice_col + j.
+  // Wave w's instruction i fills slice rows 64 w + 16 i + l / 4 (logical chunk (l % 4) ^ key into
+  // physical chunk l % 4, key = (l / 8) % 4); its scale instruction the words of rows 64 w + l.
   const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSliceRows / 2 : kSliceRows);
-  const int64_t wave_col = slice_col + wave * (kGated ? 32 : 64);
   auto weight_row = [&](int j) -> int64_t {
-    if constexpr (kGated) return j < 32 ? wave_col + j : p.out_width + wave_col + j - 32;
-    else return wave_col + j;
+    if constexpr (kGated) {
+      const int64_t col = slice_col + 64 * (j >> 7) + (j & 63);
+      return (j & 64) ? p.out_width + col : col;
+    } else {
+      return slice_col + j;
+    }
   };
   const uint8_t *expert_weights = p.weights + expert * p.n_total * weight_row_bytes;
-  const uint32_t w_off = static_cast<uint32_t>((lane / 4) * weight_row_bytes + ((lane & 3) ^ ((lane >> 4) & 3)) * 16);
+  const uint32_t w_off = static_cast<uint32_t>((lane / 4) * weight_row_bytes + ((lane & 3) ^ ((lane >> 3) & 3)) * 16);
   const uint8_t *expert_scales = p.weight_scales + expert * p.n_total * scale_row_bytes;
-  const uint32_t ws_off = static_cast<uint32_t>(weight_row(lane) * scale_row_bytes);
+  const uint32_t ws_off = static_cast<uint32_t>(weight_row(64 * wave + lane) * scale_row_bytes);
 
   auto issue = [&](MxStage &st, int k) {
-    const uint32_t act_lds = lds_address(st.act + wave * 2 * kWave);
+    const uint32_t act_lds = lds_address(st.act + wave * 4 * kWave);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
       dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
     const uint32_t weight_lds = lds_address(st.weights + wave * 64 * 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dma16(expert_weights + weight_row(16 * i) * weight_row_bytes + static_cast<int64_t>(k) * 64, w_off,
+      dma16(expert_weights + weight_row(64 * wave + 16 * i) * weight_row_bytes + static_cast<int64_t>(k) * 64, w_off,
             __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
     dma4(expert_scales + static_cast<int64_t>(k) * 4, ws_off,
-                 __builtin_amdgcn_readfirstlane(lds_address(st.weight_scales + wave * 64)));
+         __builtin_amdgcn_readfirstlane(lds_address(st.weight_scales + wave * 64)));
     dma4(p.act_scales + static_cast<int64_t>(k) * 4, as_off,
-                 __builtin_amdgcn_readfirstlane(lds_address(st.act_scales + wave * kWave)));
+         __builtin_amdgcn_readfirstlane(lds_address(st.act_scales + wave * kWave)));
   };
 
-  floatx4 acc[8][4];
+  floatx4 acc[4][8];
 #pragma unroll
-  for (int tb = 0; tb < 8; ++tb)
+  for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int jb = 0; jb < 8; ++jb) acc[tb][jb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](const MxStage &st) {
-    u32x4 wf[4];
-    uint32_t sw[4];
+    u32x4 wf[8];
+    uint32_t sw[8];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const int row = wave * 64 + jb * 16 + r16;
+    for (int jb = 0; jb < 8; ++jb) {
+      const int row = ww * 128 + jb * 16 + r16;
       wf[jb] = st.weights[weight_slot(row, g)];
       sw[jb] = reinterpret_cast<const uint8_t *>(st.weight_scales)[row * 4 + g];
     }
 #pragma unroll
-    for (int tb = 0; tb < 8; ++tb) {
-      const int row = tb * 16 + r16;
+    for (int tb = 0; tb < 4; ++tb) {
+      const int row = wt * 64 + tb * 16 + r16;
       const u32x4 lo = st.act[act_slot(row, g)];
       const u32x4 hi = st.act[act_slot(row, g + 4)];
       const intx8 x = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                             static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-      const uint32_t sx = reinterpret_cast<const uint8_t *>(st.act_scales)[(tb * kWave + r16) * 4 + g];
+      const uint32_t sx = reinterpret_cast<const uint8_t *>(st.act_scales)[act_scale_slot(row) * 4 + g];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = mfma_mx(wf[jb], x, sw[jb], sx, acc[tb][jb]);
+      for (int jb = 0; jb < 8; ++jb) acc[tb][jb] = mfma_mx(wf[jb], x, sw[jb], sx, acc[tb][jb]);
     }
   };
 
-  // ---- the K loop: at the top of stage k, stages k and k + 1 are in flight; wait for k (loads
-  // land in issue order), then the barrier: every wave's stage k has landed and every wave is done
-  // with stage k - 1, whose buffer takes stage k + 2. Issues past the last stage re-read it, so
-  // every wait counts the same loads. ----
+  // ---- the K loop: at the top of stage k only stage k is in flight; once it has landed for every
+  // wave (own wait, then the barrier, which also retires every wave's reads of stage k - 1), stage
+  // k + 1 is issued into the other buffer. The issue past the last stage re-reads it, so every wait
+  // counts the same loads. ----
   issue(ring[0], 0);
-  issue(ring[1], min(1, stages - 1));
   for (int k = 0; k < stages; ++k) {
-    prefill::wait_loads_but<kTiledLoads>();
+    prefill::wait_all_loads();
     __syncthreads();
-    issue(ring[(k + 2) % kTiledStages], min(k + 2, stages - 1));
-    compute(ring[k % kTiledStages]);
+    issue(ring[(k + 1) & 1], min(k + 1, stages - 1));
+    compute(ring[k & 1]);
   }
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done reading the stage buffers
 
-  // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, token row 16 tb + r16
-  // and the wave's weight rows 16 jb + 4 g + i in element i. The output tile goes through LDS so
-  // the global stores are whole rows; LDS rows are padded by 32 bytes. ----
+  // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row
+  // 64 t + 16 tb + r16 and the wave's weight rows 16 jb + 4 g + i in element i. The output tile goes
+  // through LDS so the global stores are whole rows; LDS rows are padded by 16 bytes. ----
   constexpr int kOutCols = kGated ? kSliceRows / 2 : kSliceRows;
-  constexpr int kOutStride = kOutCols * 2 + 32;
+  constexpr int kOutStride = kOutCols * 2 + 16;
   static_assert(kTileRows * kOutStride <= static_cast<int>(sizeof(ring)), "the output tile fits the stages");
   char *tile_lds = reinterpret_cast<char *>(ring);
 #pragma unroll
-  for (int tb = 0; tb < 8; ++tb) {
-    char *row = tile_lds + (tb * 16 + r16) * kOutStride;
+  for (int tb = 0; tb < 4; ++tb) {
+    char *row = tile_lds + (wt * 64 + tb * 16 + r16) * kOutStride;
     if constexpr (kGated) {
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
+      for (int jb = 0; jb < 4; ++jb) {
         floatx4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + 2][i]) * acc[tb][jb][i];
-        store_bf16x4(reinterpret_cast<uint16_t *>(row + (wave * 32 + jb * 16 + 4 * g) * 2), v);
+        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + 4][i]) * acc[tb][jb][i];
+        store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * 64 + jb * 16 + 4 * g) * 2), v);
       }
     } else {
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-        store_bf16x4(reinterpret_cast<uint16_t *>(row + (wave * 64 + jb * 16 + 4 * g) * 2), acc[tb][jb]);
+      for (int jb = 0; jb < 8; ++jb)
+        store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * 128 + jb * 16 + 4 * g) * 2), acc[tb][jb]);
     }
   }
   __syncthreads();
@@ -523,7 +530,7 @@ __global__ void __launch_bounds__(kTiledThreads) tiled_mx_kernel(MxTiledParams t
   }
 }
 
-/// Whether the tiled kernel serves the shape: whole 128-K stages and whole 512-row weight slices.
+/// Whether the tiled kernel serves the shape: whole 128-K stages and whole 256-row weight slices.
 bool tiled_fits(bool gated, int64_t K, int64_t out_width) {
   return K % 128 == 0 && K > 0 && out_width % (gated ? kSliceRows / 2 : kSliceRows) == 0;
 }
