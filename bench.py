@@ -94,9 +94,13 @@ class Workload:
             self.scales = dict(up_gate_scales=s1, down_scales=s2)
         elif self.wdtype == "f4e2m1":
             # Setup, not timed: OCP MXFP4 (E2M1 pairs, an E8M0 scale per 32 along K).
+            # Scales converted once, at load, to the stage-major layout the prefill kernel fetches
+            # a stage of 256 rows from as one run (the decode kernel reads either).
             self.up_gate, s1 = quantize_blocks_mxfp4(self.up_gate_bf16)
             self.down, s2 = quantize_blocks_mxfp4(self.down_bf16)
-            self.scales = dict(up_gate_scales=s1, down_scales=s2)
+            self.scales = dict(up_gate_scales=ops.mx_stage_major_scales(s1), down_scales=ops.mx_stage_major_scales(s2),
+                               scale_layout="stage")
+            self.row_major_scales = (s1, s2)
         else:
             self.up_gate, self.down = self.up_gate_bf16, self.down_bf16
         self.layer = ops.MoeLayer(H, E, self.top, I, T, weight_dtype=self.wdtype)
@@ -184,8 +188,11 @@ def cpu_baseline(w, runs):
     x, router = bits(w.x), bits(w.router)
     if w.wdtype in ("f8e4m3", "f4e2m1"):
         up_gate, down = w.up_gate.cpu().numpy(), w.down.cpu().numpy()
-        s1 = w.scales["up_gate_scales"].cpu().numpy()
-        s2 = w.scales["down_scales"].cpu().numpy()
+        if w.wdtype == "f4e2m1":
+            s1, s2 = (t.cpu().numpy() for t in w.row_major_scales)
+        else:
+            s1 = w.scales["up_gate_scales"].cpu().numpy()
+            s2 = w.scales["down_scales"].cpu().numpy()
     else:
         up_gate, down, s1, s2 = bits(w.up_gate), bits(w.down), None, None
     oracle_lib.moe_layer(x[:1], router, up_gate, down, w.top, up_gate_scales=s1, down_scales=s2)  # warm

@@ -39,6 +39,7 @@ struct uniserve_moe_layer_call {
   int64_t renormalize;
   int64_t weight_dtype;        ///< UNISERVE_DTYPE_BF16, _F8E4M3 or _F4E2M1
   int64_t multiprocessors;
+  int64_t weight_scale_layout; ///< MXFP4: uniserve_mx_scale_layout of both scale tables; else 0
   char error[512];
 };
 
@@ -63,14 +64,17 @@ struct uniserve_moe_layer_views {
   int64_t gated;               ///< [permuted_rows, intermediate] bf16
   int64_t products;            ///< [permuted_rows, hidden_size] bf16
   int64_t hidden_q;            ///< fp8 and MX: [tokens, hidden_size] e4m3
-  int64_t hidden_s;            ///< fp8: [tokens, hidden_size / 128] f32; MX: [tokens, hidden_size / 32] E8M0
+  int64_t hidden_s;            ///< fp8: [tokens, hidden_size / 128] f32; MX: [tokens, hidden_size / 32]
+                               ///< E8M0, or with route_scales stage-major by permuted row
+                               ///< [hidden_size / 128, permuted_rows, 4]
   int64_t gated_q;             ///< fp8: [permuted_rows, intermediate] e4m3
-  int64_t gated_s;             ///< MX: [permuted_rows, intermediate / 32] E8M0;
-                               ///< fp8: [permuted_rows, intermediate / 128] f32, or with
-                               ///< route_scales [intermediate / 128, permuted_rows]
+  int64_t gated_s;             ///< fp8: [permuted_rows, intermediate / 128] f32, or with
+                               ///< route_scales [intermediate / 128, permuted_rows];
+                               ///< MX: [permuted_rows, intermediate / 32] E8M0, or with route_scales
+                               ///< [intermediate / 128, permuted_rows, 4]
   int64_t hidden_route_s;      ///< fp8 with route_scales: [hidden_size / 128, permuted_rows] f32,
                                ///< the scale of each route's token by permuted row; else -1
-  int64_t route_scales;        ///< 1 when the fp8 products take their activation scales
+  int64_t route_scales;        ///< 1 when the fp8 or MX products take their activation scales
                                ///< route-major (prefill shapes), else 0
   int64_t max_tiles;
   int64_t permuted_rows;

@@ -24,6 +24,18 @@
 
 #include "uniserve_abi.h"
 
+/// Layouts of an MXFP4 stack's E8M0 scale table ([stacks, rows, K / 32] bytes either way).
+///  * ROW_MAJOR: scale of (stack s, row n, block b) at (s * rows + n) * K/32 + b - the OCP /
+///    checkpoint layout.
+///  * STAGE_MAJOR: the four blocks of one 128-element stage of a row are one 4-byte word, and a
+///    stage's words of all rows are contiguous: (s, n, b) at ((s * K/128 + b / 4) * rows + n) * 4
+///    + b % 4. The prefill kernel then fetches a stage's scales of 256 weight rows as one 1 KB run
+///    instead of one cache line per row (uniserve_mx_stage_major_scales converts, once, at load).
+enum uniserve_mx_scale_layout {
+  UNISERVE_MX_SCALES_ROW_MAJOR = 0,
+  UNISERVE_MX_SCALES_STAGE_MAJOR = 1,
+};
+
 /// Rows quantised per 32 contiguous channels to MXFP8: out[r, c] = e4m3(in[r, c] / 2^(s - 127)),
 /// s = scales[r, c / 32]. Rows at or past `*row_limit` (when given) are left untouched.
 struct uniserve_quantize_mxfp8_call {
@@ -58,6 +70,7 @@ struct uniserve_gather_mx_call {
   int64_t top;
   int64_t out_dtype;                    ///< bf16
   int64_t multiprocessors;
+  int64_t weight_scale_layout;          ///< uniserve_mx_scale_layout of weight_scales
   char error[512];
 };
 
@@ -78,9 +91,21 @@ struct uniserve_route_mx_call {
   int64_t experts;
   int64_t out_dtype;
   int64_t multiprocessors;
+  int64_t weight_scale_layout;          ///< uniserve_mx_scale_layout of weight_scales
+  char error[512];
+};
+
+/// Converts a ROW_MAJOR scale table to STAGE_MAJOR (see uniserve_mx_scale_layout).
+struct uniserve_mx_stage_scales_call {
+  const uint8_t *in;                    ///< [stacks, rows, width / 32] E8M0, row-major
+  uint8_t *out;                         ///< the same bytes, stage-major
+  int64_t stacks;
+  int64_t rows;
+  int64_t width;                        ///< K, a multiple of 128
   char error[512];
 };
 
 UNISERVE_EXTERN_C int32_t uniserve_quantize_mxfp8(const struct uniserve_quantize_mxfp8_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_gather_gemm_mx(const struct uniserve_gather_mx_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_route_gemm_mx(const struct uniserve_route_mx_call *call, void *stream);
+UNISERVE_EXTERN_C int32_t uniserve_mx_stage_major_scales(const struct uniserve_mx_stage_scales_call *call, void *stream);

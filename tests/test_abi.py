@@ -191,3 +191,54 @@ def test_sigmoid_gated_add_refusals():
     assert lib.uniserve_sigmoid_gated_add_launch(p, p, p, 4, 8, abi.DTYPE["f8e4m3"], None, error, 512) != 0
     assert b"bf16, f16 or f32" in error.value
     assert lib.uniserve_sigmoid_gated_add_launch(None, None, None, 0, 8, abi.DTYPE["bf16"], None, error, 512) == 0
+
+
+# The call structures of this library's own entries (no reference layout to assert against): the
+# C compiler's sizes and offsets, read from a program built against include/*.h, are the mirror's.
+OWN = {
+    "uniserve_quantize_fp8_call": (abi.QuantizeFp8Call, {}),
+    "uniserve_gather_fp8_call": (abi.GatherFp8Call, {}),
+    "uniserve_route_fp8_call": (abi.RouteFp8Call, {}),
+    "uniserve_quantize_mxfp8_call": (abi.QuantizeMxfp8Call, {}),
+    "uniserve_gather_mx_call": (abi.GatherMxCall, {}),
+    "uniserve_route_mx_call": (abi.RouteMxCall, {}),
+    "uniserve_mx_stage_scales_call": (abi.MxStageScalesCall, {"input": "in"}),
+    "uniserve_moe_layer_call": (abi.LayerCall, {}),
+    "uniserve_moe_layer_views": (abi.LayerViews, {}),
+    "uniserve_moe_sort_call": (abi.SortCall, {}),
+    "uniserve_gather_call": (abi.GatherCall, {}),
+    "uniserve_route_call": (abi.RouteCall, {}),
+    "uniserve_unpermute_call": (abi.UnpermuteCall, {}),
+}
+
+
+def test_own_structures_match_the_compiler(tmp_path):
+    import shutil
+    import subprocess
+
+    compiler = shutil.which("g++") or shutil.which("c++")
+    if compiler is None:
+        pytest.skip("no host C++ compiler")
+    lines = ["#include <cstddef>", "#include <cstdio>"]
+    lines += [f'#include "{h.name}"' for h in HEADERS]
+    lines.append("int main() {")
+    for struct, (mirror, renames) in OWN.items():
+        lines.append(f'  std::printf("%s size %zu\\n", "{struct}", sizeof({struct}));')
+        for field, _ in mirror._fields_:
+            name = renames.get(field, field)
+            lines.append(f'  std::printf("%s %s %zu\\n", "{struct}", "{field}", offsetof({struct}, {name}));')
+    lines.append("  return 0;\n}")
+    source = tmp_path / "layouts.cpp"
+    source.write_text("\n".join(lines) + "\n")
+    binary = tmp_path / "layouts"
+    subprocess.run([compiler, "-std=c++17", "-I", str(ROOT / "include"), str(source), "-o", str(binary)], check=True)
+    output = subprocess.run([str(binary)], check=True, capture_output=True, text=True).stdout.split("\n")
+    measured = {}
+    for line in output:
+        if line:
+            struct, field, value = line.split()
+            measured[(struct, field)] = int(value)
+    for struct, (mirror, _) in OWN.items():
+        assert ctypes.sizeof(mirror) == measured[(struct, "size")], struct
+        for field, _ in mirror._fields_:
+            assert getattr(mirror, field).offset == measured[(struct, field)], (struct, field)

@@ -53,11 +53,21 @@ def mx_stacks(device, experts, hidden, intermediate, seed=2):
     return q1, s1, q2, s2
 
 
-@pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew", [
-    (64, 2048, 128, 8, 768, "uniform"), (1, 4096, 128, 8, 1536, "uniform"), (512, 2048, 128, 8, 768, "zipf"),
-    (1024, 4096, 128, 8, 1536, "zipf")])
-def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew):
-    announce("mx products", tokens, hidden, experts, top, intermediate, skew)
+def test_stage_major_scales_are_the_row_major_bytes_regrouped(device):
+    announce("mx stage-major scales")
+    rng = np.random.default_rng(3)
+    table = rng.integers(0, 256, size=(3, 192, 1536 // 32), dtype=np.uint8)
+    got = ops.mx_stage_major_scales(torch.from_numpy(table).to(device)).cpu().numpy()
+    want = table.reshape(3, 192, 1536 // 128, 4).transpose(0, 2, 1, 3)
+    np.testing.assert_array_equal(got.reshape(3, 1536 // 128, 192, 4), want)
+
+
+@pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew,layout", [
+    (64, 2048, 128, 8, 768, "uniform", "row"), (1, 4096, 128, 8, 1536, "uniform", "row"),
+    (512, 2048, 128, 8, 768, "zipf", "row"), (1024, 4096, 128, 8, 1536, "zipf", "row"),
+    (64, 2048, 128, 8, 768, "uniform", "stage"), (512, 2048, 128, 8, 768, "zipf", "stage")])
+def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew, layout):
+    announce("mx products", tokens, hidden, experts, top, intermediate, skew, layout)
     rng = np.random.default_rng(tokens + 7)
     if skew == "zipf":
         p = np.exp(zipf_bias(experts).astype(np.float64))
@@ -72,12 +82,15 @@ def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew):
     maps = ops.moe_sort(ids, weights, experts)
     rows = ops.permuted_rows(tokens, top, experts)
     d = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    ws1, ws2 = d(s1), d(s2)
+    if layout == "stage":
+        ws1, ws2 = ops.mx_stage_major_scales(ws1), ops.mx_stage_major_scales(ws2)
     gated = torch.full((rows, intermediate), float("nan"), dtype=torch.bfloat16, device=device)
-    ops.gather_gemm_mx(xq, xs, d(q1), d(s1), top, maps, rows, out=gated)
+    ops.gather_gemm_mx(xq, xs, d(q1), ws1, top, maps, rows, out=gated, scale_layout=layout)
     padded_t = maps[ops.TOTAL_PADDED_TOKENS][:1]
     gq, gs = ops.quantize_mxfp8(torch.nan_to_num(gated, 0.0), row_limit=padded_t)
     products = torch.full((rows, hidden), float("nan"), dtype=torch.bfloat16, device=device)
-    ops.route_gemm_mx(gq, gs, d(q2), d(s2), maps, out=products)
+    ops.route_gemm_mx(gq, gs, d(q2), ws2, maps, out=products, scale_layout=layout)
     torch.cuda.synchronize()
 
     sort = sort_on_host(maps, tokens, top)
@@ -93,10 +106,12 @@ def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew):
 
 
 MX_LAYERS = {
-    # name: tokens, hidden, experts, top, intermediate, zipf, oracle sample
-    "30b decode mx": (64, 2048, 128, 8, 768, False, None),
-    "30b prefill mx zipf": (8192, 2048, 128, 8, 768, True, 96),
-    "235b decode mx one token": (1, 4096, 128, 8, 1536, False, None),
+    # name: tokens, hidden, experts, top, intermediate, zipf, oracle sample, weight scale layout
+    "30b decode mx": (64, 2048, 128, 8, 768, False, None, "row"),
+    "30b prefill mx zipf": (8192, 2048, 128, 8, 768, True, 96, "row"),
+    "235b decode mx one token": (1, 4096, 128, 8, 1536, False, None, "row"),
+    "30b decode mx stage scales": (64, 2048, 128, 8, 768, False, None, "stage"),
+    "30b prefill mx zipf stage scales": (8192, 2048, 128, 8, 768, True, 96, "stage"),
 }
 
 
@@ -116,13 +131,17 @@ def test_mx_layer_against_the_oracle(device, case):
     """The whole layer over MXFP4 stacks against the oracle's composition: router ids bit-exact;
     outputs within 4e-2 of the peak (the gated rows are re-quantised to MXFP8 on both sides from
     bf16 values that may differ in their last bit, which moves a code by one step)."""
-    tokens, hidden, experts, top, intermediate, zipf, sample = MX_LAYERS[case]
+    tokens, hidden, experts, top, intermediate, zipf, sample, layout = MX_LAYERS[case]
     announce("mx layer", case)
     x, router, host_w = mx_layer_inputs(device, tokens, hidden, experts, intermediate)
     w1, s1, w2, s2 = on(device, host_w)
+    if layout == "stage":
+        s1, s2 = ops.mx_stage_major_scales(s1), ops.mx_stage_major_scales(s2)
     bias = torch.from_numpy(zipf_bias(experts)).to(device) if zipf else None
     layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f4e2m1")
-    out = layer(x, router, w1, w2, up_gate_scales=s1, down_scales=s2, router_bias=bias)
+    out = layer(x, router, w1, w2, up_gate_scales=s1, down_scales=s2, router_bias=bias, scale_layout=layout)
+    # Prefill shapes keep both activation scale tables stage-major by permuted row.
+    assert layer.views.route_scales == (1 if tokens >= 4096 else 0)
     torch.cuda.synchronize()
     ids = layer.view("ids", torch.int32, (tokens, top)).cpu().numpy()
     got = bf16_values(out)

@@ -23,6 +23,7 @@
 //    stages of 128 K.
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "grouped_mx.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_moe_mx.h"
 
@@ -36,11 +37,16 @@ constexpr int kQuantThreads = 256;
 struct MxQuantParams {
   const void *input;
   uint8_t *out;
-  uint8_t *scales;
+  uint8_t *scales;               ///< row-major [rows, width / 32], or null
   const int32_t *row_limit;
   int64_t rows;
   int64_t width;
   int32_t input_f32;
+  uint8_t *stage_scales;         ///< or null: stage-major [width / 128, stage_rows, 4]
+  const int32_t *routes;         ///< with stage_scales, or null: row r's scales go to stage rows
+                                 ///< routes[r * top + j] (>= 0) instead of row r
+  int64_t top;
+  int64_t stage_rows;
 };
 
 /// The E8M0 byte of a block: the smallest power of two 2^e with amax <= limit * 2^e, e in
@@ -92,7 +98,19 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_mxfp8_kernel(MxQuantPa
     const uint32_t scale = mx_scale(amax, 448.0f);
     // A power of two: the division is exact and no quotient exceeds 448.
     *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, ldexpf(1.0f, static_cast<int>(scale) - 127));
-    if (sub == 0) p.scales[block] = static_cast<uint8_t>(scale);
+    if (sub == 0 && p.scales != nullptr) p.scales[block] = static_cast<uint8_t>(scale);
+    if (p.stage_scales != nullptr) {
+      const int64_t b = block % blocks_per_row;
+      uint8_t *stage = p.stage_scales + (b / 4) * p.stage_rows * 4 + (b % 4);
+      if (p.routes == nullptr) {
+        if (sub == 0) stage[row * 4] = static_cast<uint8_t>(scale);
+      } else {
+        for (int64_t j = sub; j < p.top; j += 4) {
+          const int32_t at = p.routes[row * p.top + j];
+          if (at >= 0) stage[static_cast<int64_t>(at) * 4] = static_cast<uint8_t>(scale);
+        }
+      }
+    }
   }
 }
 
@@ -105,9 +123,9 @@ constexpr int64_t kSplitBelow = 512;    // workgroups under which K is split ove
 
 struct MxParams {
   const uint8_t *act;            ///< FC1: [tokens, K] e4m3; FC2: [permuted_rows, K]
-  const uint8_t *act_scales;     ///< [rows of act, K / 32] E8M0
+  const uint8_t *act_scales;     ///< E8M0, see as_stage / as_row
   const uint8_t *weights;        ///< [experts, n_total, K / 2] E2M1 pairs
-  const uint8_t *weight_scales;  ///< [experts, n_total, K / 32] E8M0
+  const uint8_t *weight_scales;  ///< E8M0, [experts, n_total, K / 32] bytes in either layout
   uint16_t *out;                 ///< [permuted_rows, out_width] bf16
   const int32_t *tile_to_expert;
   const int32_t *tile_to_limit;
@@ -117,7 +135,25 @@ struct MxParams {
   int64_t n_total;
   int64_t out_width;
   int64_t top;
+  // The 4-byte word of a row's scales of 128-element stage k sits at k * stage + row * row_bytes
+  // (row-major: stage 4, row K / 32; stage-major: stage rows * 4, row 4), per expert for weights.
+  int64_t ws_stage;
+  int64_t ws_row;
+  int64_t as_stage;
+  int64_t as_row;
+  int32_t as_by_route;           ///< activation scale rows are permuted rows, not act rows
 };
+
+/// Stride words of a scale table with `rows` rows in `layout`.
+inline void scale_strides(int64_t layout, int64_t rows, int64_t K, int64_t *stage, int64_t *row) {
+  if (layout == UNISERVE_MX_SCALES_STAGE_MAJOR) {
+    *stage = rows * 4;
+    *row = 4;
+  } else {
+    *stage = 4;
+    *row = K / 32;
+  }
+}
 
 __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
   uint2 packed;
@@ -186,10 +222,10 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   const bool upper = r16 >= 8;
   const int source0 = (r16 & 7) * 8 + g;  // piece g (MFMA h = 0)
   const int source1 = source0 + 4;        // piece g + 4 (MFMA h = 1)
-  // This lane's weight scales: its row r16 of each set, eight E8M0 bytes per chunk.
+  // This lane's weight scales: its row r16 of each set, two 4-byte stage words per chunk.
   const uint8_t *ws[2];
-  ws[0] = p.weight_scales + (expert * p.n_total + n0 + r16) * scale_row_bytes;
-  ws[1] = p.weight_scales + (expert * p.n_total + n1 + r16) * scale_row_bytes;
+  ws[0] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n0 + r16) * p.ws_row;
+  ws[1] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n1 + r16) * p.ws_row;
 
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint8_t *a[kPassTiles];
@@ -203,7 +239,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
       if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
       if (!valid[ms]) source = 0;
       a[ms] = p.act + source * p.K + g * 16;
-      as[ms] = p.act_scales + source * scale_row_bytes;
+      as[ms] = p.act_scales + (p.as_by_route ? first + (valid[ms] ? m : 0) : source) * p.as_row;
     }
     floatx4 acc[2][kPassTiles];
 #pragma unroll
@@ -226,7 +262,9 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
         d.lines[i] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * weight_row_bytes + c * 128));
 #pragma unroll
-      for (int s = 0; s < 2; ++s) d.wscale[s] = *reinterpret_cast<const uint2 *>(ws[s] + c * 8);
+      for (int s = 0; s < 2; ++s)
+        d.wscale[s] = uint2{*reinterpret_cast<const uint32_t *>(ws[s] + 2 * c * p.ws_stage),
+                            *reinterpret_cast<const uint32_t *>(ws[s] + (2 * c + 1) * p.ws_stage)};
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) {
 #pragma unroll
@@ -240,7 +278,9 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
             d.x[ms][h] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
           }
         }
-        d.xscale[ms] = valid[ms] ? *reinterpret_cast<const uint2 *>(as[ms] + c * 8) : uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
+        d.xscale[ms] = valid[ms] ? uint2{*reinterpret_cast<const uint32_t *>(as[ms] + 2 * c * p.as_stage),
+                                         *reinterpret_cast<const uint32_t *>(as[ms] + (2 * c + 1) * p.as_stage)}
+                                 : uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
       }
     };
     // Byte 4 h + g of an 8-byte scale word: this lane's block of MFMA h.
@@ -327,8 +367,6 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
 // multiplies, one barrier per stage. Chunk c of a row sits at c ^ key(row) (activation rows:
 // (r >> 1) & 7; weight rows: (r >> 1) & 3, both measured free of bank conflicts for these reads).
 
-constexpr int kTiledWaves = 4;
-constexpr int kTiledThreads = kTiledWaves * kWave;
 constexpr int kSliceRows = 256;                       // weight rows per workgroup
 
 struct MxTiledParams {
@@ -339,16 +377,17 @@ struct MxTiledParams {
   int32_t groups_per_xcd;
 };
 
+/// One stage of kWaves waves: wave w's scale instruction writes 64 words at 64 w (its rows first).
+template <int kWaves>
 struct MxStage {
   u32x4 act[kTileRows * 8];        // 16 KB
   u32x4 weights[kSliceRows * 4];   // 16 KB
-  uint32_t weight_scales[kSliceRows];
-  uint32_t act_scales[kTiledWaves * kWave];  // tile row r at 64 (r / 32) + r % 32
+  uint32_t weight_scales[kWaves * kWave];
+  uint32_t act_scales[kWaves * kWave];
 };
 
 __device__ __forceinline__ int act_slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
 __device__ __forceinline__ int weight_slot(int row, int chunk) { return row * 4 + (chunk ^ ((row >> 1) & 3)); }
-__device__ __forceinline__ int act_scale_slot(int row) { return (row >> 5) * kWave + (row & 31); }
 
 /// One 4-byte DMA per lane from `base` + `offset` into LDS at `lds` + 4 * lane (see `dma16`).
 __device__ __forceinline__ void dma4(const void *base, uint32_t offset, uint32_t lds) {
@@ -361,12 +400,23 @@ __device__ __forceinline__ void dma4(const void *base, uint32_t offset, uint32_t
       : "m0");
 }
 
-template <bool kGated>
-__global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParams tp) {
+/// kWaves = 4, kStages = 2: two workgroups per CU. kWaves = 8, kStages = 4: one workgroup per CU
+/// with three stages in flight.
+template <bool kGated, int kWaves, int kStages>
+__global__ void __launch_bounds__(kWaves * kWave, 8 / kWaves) tiled_mx_kernel(MxTiledParams tp) {
   using prefill::dma16;
   using prefill::lds_address;
+  constexpr int kThreadsHere = kWaves * kWave;
+  constexpr int kRowsPerWave = kSliceRows / (kWaves / 2);  // weight rows of one wave (2 x kWaves/2)
+  constexpr int kBlocks = kRowsPerWave / 16;               // its 16-row weight blocks
+  constexpr int kCols = kRowsPerWave / 2;                  // FC1: its up (and gate) rows
+  constexpr int kActLoads = 16 / kWaves;                   // 8-row activation DMAs per wave
+  constexpr int kWeightLoads = 16 / kWaves;                // 16-row weight DMAs per wave
+  constexpr int kLoads = kActLoads + kWeightLoads + 2;
+  constexpr int kActRows = kTileRows / kWaves;             // rows whose scales a wave brings
+  constexpr int kWeightRows = kSliceRows / kWaves;
   const MxParams &p = tp.base;
-  __shared__ MxStage ring[2];
+  __shared__ MxStage<kWaves> ring[kStages];
 
   // ---- the work item: groups of `group` tiles, slice-major inside a group, dealt to the XCDs in
   // turn (block b runs on XCD b % 8) ----
@@ -389,7 +439,7 @@ __global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParam
   const int t = static_cast<int>(threadIdx.x);
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int wt = wave & 1;   // token half
-  const int ww = wave >> 1;  // weight half
+  const int ww = wave >> 1;  // weight part
   const int lane = lane_id();
   const int r16 = lane & 15;
   const int g = lane >> 4;
@@ -409,25 +459,30 @@ __global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParam
   };
 
   // ---- DMA sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
-  // Activations: wave w's instruction i fills tile rows 32 w + 8 i + l / 8, lane l bringing logical
-  // chunk (l % 8) ^ key(row) into physical chunk l % 8; its scale instruction brings the scale
-  // words of rows 32 w + l % 32 (lanes 32.. repeat them into the padding).
-  uint32_t a_off[4];
+  // Activations: wave w's instruction i fills tile rows 8 (kActLoads w + i) + l / 8, lane l
+  // bringing logical chunk (l % 8) ^ key(row) into physical chunk l % 8; its scale instruction
+  // brings the scale words of tile rows kActRows w + l % kActRows (the other lanes repeat them into
+  // the padding).
+  uint32_t a_off[kActLoads];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 32 * wave + 8 * i + lane / 8;
+  for (int i = 0; i < kActLoads; ++i) {
+    const int r = 8 * (kActLoads * wave + i) + lane / 8;
     a_off[i] = static_cast<uint32_t>(source_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
   }
-  const uint32_t as_off = static_cast<uint32_t>(source_row(32 * wave + (lane & 31)) * scale_row_bytes);
-  // Weights: slice row j (0..255) is, for FC1, up row col(j) or gate row out_width + col(j) with
-  // col(j) = slice_col + 64 (j / 128) + j % 64 (up for j % 128 < 64); for FC2, row slice_col + j.
-  // Wave w's instruction i fills slice rows 64 w + 16 i + l / 4 (logical chunk (l % 4) ^ key into
-  // physical chunk l % 4, key = (l / 8) % 4); its scale instruction the words of rows 64 w + l.
+  const int as_r = kActRows * wave + lane % kActRows;
+  const uint32_t as_off = static_cast<uint32_t>(
+      (p.as_by_route ? first + (as_r < rows ? as_r : 0) : source_row(as_r)) * p.as_row);
+  // Weights: slice row j = kRowsPerWave w + jj belongs to wave part w: for FC1 jj < kCols is up row
+  // col and jj >= kCols gate row out_width + col, col = slice_col + kCols w + jj % kCols; for FC2
+  // row slice_col + j. Wave w's instruction i fills slice rows 16 (kWeightLoads w + i) + l / 4
+  // (logical chunk (l % 4) ^ key into physical chunk l % 4, key = (l / 8) % 4); its scale
+  // instruction the words of rows kWeightRows w + l % kWeightRows.
   const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSliceRows / 2 : kSliceRows);
   auto weight_row = [&](int j) -> int64_t {
     if constexpr (kGated) {
-      const int64_t col = slice_col + 64 * (j >> 7) + (j & 63);
-      return (j & 64) ? p.out_width + col : col;
+      const int jj = j % kRowsPerWave;
+      const int64_t col = slice_col + kCols * (j / kRowsPerWave) + jj % kCols;
+      return jj >= kCols ? p.out_width + col : col;
     } else {
       return slice_col + j;
     }
@@ -435,38 +490,38 @@ __global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParam
   const uint8_t *expert_weights = p.weights + expert * p.n_total * weight_row_bytes;
   const uint32_t w_off = static_cast<uint32_t>((lane / 4) * weight_row_bytes + ((lane & 3) ^ ((lane >> 3) & 3)) * 16);
   const uint8_t *expert_scales = p.weight_scales + expert * p.n_total * scale_row_bytes;
-  const uint32_t ws_off = static_cast<uint32_t>(weight_row(64 * wave + lane) * scale_row_bytes);
+  const uint32_t ws_off = static_cast<uint32_t>(weight_row(kWeightRows * wave + lane % kWeightRows) * p.ws_row);
 
-  auto issue = [&](MxStage &st, int k) {
-    const uint32_t act_lds = lds_address(st.act + wave * 4 * kWave);
+  auto issue = [&](MxStage<kWaves> &st, int k) {
+    const uint32_t act_lds = lds_address(st.act + wave * kActLoads * kWave);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kActLoads; ++i)
       dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
-    const uint32_t weight_lds = lds_address(st.weights + wave * 64 * 4);
+    const uint32_t weight_lds = lds_address(st.weights + wave * kWeightLoads * kWave);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(expert_weights + weight_row(64 * wave + 16 * i) * weight_row_bytes + static_cast<int64_t>(k) * 64, w_off,
-            __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
-    dma4(expert_scales + static_cast<int64_t>(k) * 4, ws_off,
-         __builtin_amdgcn_readfirstlane(lds_address(st.weight_scales + wave * 64)));
-    dma4(p.act_scales + static_cast<int64_t>(k) * 4, as_off,
+    for (int i = 0; i < kWeightLoads; ++i)
+      dma16(expert_weights + weight_row(16 * (kWeightLoads * wave + i)) * weight_row_bytes + static_cast<int64_t>(k) * 64,
+            w_off, __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
+    dma4(expert_scales + static_cast<int64_t>(k) * p.ws_stage, ws_off,
+         __builtin_amdgcn_readfirstlane(lds_address(st.weight_scales + wave * kWave)));
+    dma4(p.act_scales + static_cast<int64_t>(k) * p.as_stage, as_off,
          __builtin_amdgcn_readfirstlane(lds_address(st.act_scales + wave * kWave)));
   };
 
-  floatx4 acc[4][8];
+  floatx4 acc[4][kBlocks];
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int jb = 0; jb < 8; ++jb) acc[tb][jb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int jb = 0; jb < kBlocks; ++jb) acc[tb][jb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](const MxStage &st) {
-    u32x4 wf[8];
-    uint32_t sw[8];
+  auto compute = [&](const MxStage<kWaves> &st) {
+    u32x4 wf[kBlocks];
+    uint32_t sw[kBlocks];
 #pragma unroll
-    for (int jb = 0; jb < 8; ++jb) {
-      const int row = ww * 128 + jb * 16 + r16;
+    for (int jb = 0; jb < kBlocks; ++jb) {
+      const int row = ww * kRowsPerWave + jb * 16 + r16;
       wf[jb] = st.weights[weight_slot(row, g)];
-      sw[jb] = reinterpret_cast<const uint8_t *>(st.weight_scales)[row * 4 + g];
+      sw[jb] = reinterpret_cast<const uint8_t *>(st.weight_scales)[((row / kWeightRows) * kWave + row % kWeightRows) * 4 + g];
     }
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -475,22 +530,24 @@ __global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParam
       const u32x4 hi = st.act[act_slot(row, g + 4)];
       const intx8 x = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                             static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-      const uint32_t sx = reinterpret_cast<const uint8_t *>(st.act_scales)[act_scale_slot(row) * 4 + g];
+      const uint32_t sx = reinterpret_cast<const uint8_t *>(st.act_scales)[((row / kActRows) * kWave + row % kActRows) * 4 + g];
 #pragma unroll
-      for (int jb = 0; jb < 8; ++jb) acc[tb][jb] = mfma_mx(wf[jb], x, sw[jb], sx, acc[tb][jb]);
+      for (int jb = 0; jb < kBlocks; ++jb) acc[tb][jb] = mfma_mx(wf[jb], x, sw[jb], sx, acc[tb][jb]);
     }
   };
 
-  // ---- the K loop: at the top of stage k only stage k is in flight; once it has landed for every
-  // wave (own wait, then the barrier, which also retires every wave's reads of stage k - 1), stage
-  // k + 1 is issued into the other buffer. The issue past the last stage re-reads it, so every wait
-  // counts the same loads. ----
-  issue(ring[0], 0);
+  // ---- the K loop: at the top of stage k, stages k .. k + kStages - 2 are in flight; once stage k
+  // has landed for every wave (own wait - loads complete in issue order - then the barrier, which
+  // also retires every wave's reads of stage k - 1), stage k + kStages - 1 is issued into the
+  // buffer stage k - 1 used. Issues past the last stage re-read it, so every wait counts the same
+  // loads. ----
+#pragma unroll
+  for (int k = 0; k < kStages - 1; ++k) issue(ring[k], min(k, stages - 1));
   for (int k = 0; k < stages; ++k) {
-    prefill::wait_all_loads();
+    prefill::wait_loads_but<(kStages - 2) * kLoads>();
     __syncthreads();
-    issue(ring[(k + 1) & 1], min(k + 1, stages - 1));
-    compute(ring[k & 1]);
+    issue(ring[(k + kStages - 1) % kStages], min(k + kStages - 1, stages - 1));
+    compute(ring[k % kStages]);
   }
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done reading the stage buffers
@@ -507,21 +564,21 @@ __global__ void __launch_bounds__(kTiledThreads, 2) tiled_mx_kernel(MxTiledParam
     char *row = tile_lds + (wt * 64 + tb * 16 + r16) * kOutStride;
     if constexpr (kGated) {
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
+      for (int jb = 0; jb < kBlocks / 2; ++jb) {
         floatx4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + 4][i]) * acc[tb][jb][i];
-        store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * 64 + jb * 16 + 4 * g) * 2), v);
+        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + kBlocks / 2][i]) * acc[tb][jb][i];
+        store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * kCols + jb * 16 + 4 * g) * 2), v);
       }
     } else {
 #pragma unroll
-      for (int jb = 0; jb < 8; ++jb)
-        store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * 128 + jb * 16 + 4 * g) * 2), acc[tb][jb]);
+      for (int jb = 0; jb < kBlocks; ++jb)
+        store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * kRowsPerWave + jb * 16 + 4 * g) * 2), acc[tb][jb]);
     }
   }
   __syncthreads();
   constexpr int kPieces = kOutCols / 8;
-  for (int index = t; index < kTileRows * kPieces; index += kTiledThreads) {
+  for (int index = t; index < kTileRows * kPieces; index += kThreadsHere) {
     const int m = index / kPieces;
     const int c = index - m * kPieces;
     if (m >= rows) continue;
@@ -543,8 +600,24 @@ void launch_tiled_mx(const MxParams &p, bool gated, int64_t max_tiles, hipStream
   tp.group = 16;
   tp.groups_per_xcd = static_cast<int32_t>(ceil_div<int64_t>(ceil_div<int64_t>(max_tiles, tp.group), 8));
   const int64_t blocks = static_cast<int64_t>(tp.groups_per_xcd) * tp.group * tp.slices * 8;
-  if (gated) hipLaunchKernelGGL((tiled_mx_kernel<true>), dim3(static_cast<uint32_t>(blocks)), dim3(kTiledThreads), 0, stream, tp);
-  else hipLaunchKernelGGL((tiled_mx_kernel<false>), dim3(static_cast<uint32_t>(blocks)), dim3(kTiledThreads), 0, stream, tp);
+  constexpr int W = 4, S = 2;  // two workgroups per CU (measured better than 8 waves x 4 stages)
+  if (gated) hipLaunchKernelGGL((tiled_mx_kernel<true, W, S>), dim3(static_cast<uint32_t>(blocks)), dim3(W * kWave), 0, stream, tp);
+  else hipLaunchKernelGGL((tiled_mx_kernel<false, W, S>), dim3(static_cast<uint32_t>(blocks)), dim3(W * kWave), 0, stream, tp);
+}
+
+/// Row-major [stacks, rows, width / 32] scale bytes to stage-major: one thread per 4-byte word.
+__global__ void __launch_bounds__(256) stage_major_kernel(const uint8_t *in, uint8_t *out, int64_t stacks, int64_t rows,
+                                                          int64_t width) {
+  const int64_t stages = width / 128;
+  const int64_t words = stacks * stages * rows;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; w < words; w += stride) {
+    const int64_t n = w % rows;
+    const int64_t k = (w / rows) % stages;
+    const int64_t stack = w / (rows * stages);
+    const uint32_t word = *reinterpret_cast<const uint32_t *>(in + (stack * rows + n) * (width / 32) + k * 4);
+    *reinterpret_cast<uint32_t *>(out + w * 4) = word;
+  }
 }
 
 void launch_mx(const MxParams &p, bool gated, int64_t max_tiles, hipStream_t stream) {
@@ -563,9 +636,10 @@ void launch_mx(const MxParams &p, bool gated, int64_t max_tiles, hipStream_t str
 
 }  // namespace
 
-void launch_quantize_mxfp8(const void *input, bool input_f32, uint8_t *out, uint8_t *scales,
-                           const int32_t *row_limit, int64_t rows, int64_t width, hipStream_t stream) {
-  MxQuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0};
+void launch_quantize_mxfp8(const void *input, bool input_f32, uint8_t *out, uint8_t *scales, const int32_t *row_limit,
+                           int64_t rows, int64_t width, hipStream_t stream, uint8_t *stage_scales,
+                           const int32_t *routes, int64_t top, int64_t stage_rows) {
+  MxQuantParams p{input, out, scales, row_limit, rows, width, input_f32 ? 1 : 0, stage_scales, routes, top, stage_rows};
   const int64_t blocks = ceil_div<int64_t>(rows * (width / 32) * 4, kQuantThreads);
   const uint32_t grid = static_cast<uint32_t>(blocks < 2048 ? (blocks > 0 ? blocks : 1) : 2048);
   hipLaunchKernelGGL(quantize_mxfp8_kernel, dim3(grid), dim3(kQuantThreads), 0, stream, p);
@@ -590,8 +664,16 @@ extern "C" int32_t uniserve_quantize_mxfp8(const uniserve_quantize_mxfp8_call *c
   });
 }
 
-extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, void *stream) {
-  using namespace uniserve;
+namespace uniserve {
+
+bool mx_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate,
+                     int64_t permuted_rows) {
+  const int64_t routes_bound = permuted_rows - (kTileRows - 1) * experts;
+  return !fp8_stream_path(tokens * top, experts) && tiled_fits(true, hidden_size, intermediate) &&
+         !fp8_stream_path(routes_bound, experts) && tiled_fits(false, intermediate, hidden_size);
+}
+
+int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_mx writes bf16 only");
     if (call->hidden == nullptr || call->hidden_scales == nullptr || call->weights == nullptr ||
@@ -609,6 +691,10 @@ extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, 
       return UNISERVE_REFUSE(call, "gather_gemm_mx needs non-negative tokens and positive top and experts");
     if (call->permuted_rows < call->tokens * call->top || call->permuted_rows % kTileRows != 0)
       return UNISERVE_REFUSE(call, "gather_gemm_mx needs whole 128-row tiles that hold every route");
+    if (call->weight_scale_layout != UNISERVE_MX_SCALES_ROW_MAJOR && call->weight_scale_layout != UNISERVE_MX_SCALES_STAGE_MAJOR)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx: no weight scale layout %lld", static_cast<long long>(call->weight_scale_layout));
+    if (scale_rows != 0 && scale_rows < call->permuted_rows)
+      return UNISERVE_REFUSE(call, "gather_gemm_mx: route-major scales need a row per permuted row");
     const int64_t max_tiles = call->permuted_rows / kTileRows;
     if (max_tiles == 0) return 0;
     MxParams p{};
@@ -625,6 +711,10 @@ extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, 
     p.n_total = call->width;
     p.out_width = call->width / 2;
     p.top = call->top;
+    scale_strides(call->weight_scale_layout, p.n_total, p.K, &p.ws_stage, &p.ws_row);
+    scale_strides(scale_rows != 0 ? UNISERVE_MX_SCALES_STAGE_MAJOR : UNISERVE_MX_SCALES_ROW_MAJOR, scale_rows, p.K,
+                  &p.as_stage, &p.as_row);
+    p.as_by_route = scale_rows != 0 ? 1 : 0;
     if (!fp8_stream_path(call->tokens * call->top, call->experts) && tiled_fits(true, p.K, p.out_width))
       launch_tiled_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
     else
@@ -633,8 +723,7 @@ extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, 
   });
 }
 
-extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, void *stream) {
-  using namespace uniserve;
+int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "route_gemm_mx writes bf16 only");
     if (call->rows == nullptr || call->row_scales == nullptr || call->weights == nullptr ||
@@ -651,6 +740,10 @@ extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, vo
     if (call->experts <= 0) return UNISERVE_REFUSE(call, "route_gemm_mx needs positive experts");
     if (call->permuted_rows < 0 || call->permuted_rows % kTileRows != 0)
       return UNISERVE_REFUSE(call, "route_gemm_mx needs permuted rows of whole 128-row tiles");
+    if (call->weight_scale_layout != UNISERVE_MX_SCALES_ROW_MAJOR && call->weight_scale_layout != UNISERVE_MX_SCALES_STAGE_MAJOR)
+      return UNISERVE_REFUSE(call, "route_gemm_mx: no weight scale layout %lld", static_cast<long long>(call->weight_scale_layout));
+    if (scale_rows != 0 && scale_rows < call->permuted_rows)
+      return UNISERVE_REFUSE(call, "route_gemm_mx: route-major scales need a row per permuted row");
     const int64_t max_tiles = call->permuted_rows / kTileRows;
     if (max_tiles == 0) return 0;
     MxParams p{};
@@ -667,6 +760,10 @@ extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, vo
     p.n_total = call->width;
     p.out_width = call->width;
     p.top = 1;
+    scale_strides(call->weight_scale_layout, p.n_total, p.K, &p.ws_stage, &p.ws_row);
+    scale_strides(scale_rows != 0 ? UNISERVE_MX_SCALES_STAGE_MAJOR : UNISERVE_MX_SCALES_ROW_MAJOR, scale_rows, p.K,
+                  &p.as_stage, &p.as_row);
+    p.as_by_route = scale_rows != 0 ? 1 : 0;
     // No token count in the call: the permuted rows less one partial tile per expert bound the routes.
     const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
     if (!fp8_stream_path(routes_bound, call->experts) && tiled_fits(false, p.K, p.out_width))
@@ -674,5 +771,31 @@ extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, vo
     else
       launch_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
     return launched(call, "route_gemm_mx");
+  });
+}
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, void *stream) {
+  return uniserve::gather_gemm_mx(call, 0, stream);
+}
+
+extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, void *stream) {
+  return uniserve::route_gemm_mx(call, 0, stream);
+}
+
+extern "C" int32_t uniserve_mx_stage_major_scales(const uniserve_mx_stage_scales_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    if (call->in == nullptr || call->out == nullptr) return UNISERVE_REFUSE(call, "mx_stage_major_scales needs in and out");
+    if (call->in == call->out) return UNISERVE_REFUSE(call, "mx_stage_major_scales does not convert in place");
+    if (call->stacks < 0 || call->rows < 0 || call->width <= 0 || call->width % 128 != 0)
+      return UNISERVE_REFUSE(call, "mx_stage_major_scales needs non-negative extents and a width of whole 128-element stages");
+    const int64_t words = call->stacks * call->rows * (call->width / 128);
+    if (words == 0) return 0;
+    const int64_t blocks = ceil_div<int64_t>(words, 256);
+    hipLaunchKernelGGL(stage_major_kernel, dim3(static_cast<uint32_t>(blocks < 4096 ? blocks : 4096)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), call->in, call->out, call->stacks, call->rows, call->width);
+    return launched(call, "mx_stage_major_scales");
   });
 }

@@ -11,6 +11,7 @@
 
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "grouped_mx.hpp"
 #include "router_gemm.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_moe_fp8.h"
@@ -63,8 +64,10 @@ bool views_of(int64_t tokens, int64_t hidden, int64_t experts, int64_t top, int6
     v->route_scales = uniserve::fp8_route_scales(tokens, top, experts, hidden, intermediate, v->permuted_rows) ? 1 : 0;
     v->hidden_route_s = v->route_scales ? take(v->permuted_rows * (hidden / 128) * 4) : -1;
   } else if (weight_dtype == UNISERVE_DTYPE_F4E2M1) {
+    // Prefill shapes: both activation scale tables stage-major by permuted row.
+    v->route_scales = uniserve::mx_route_scales(tokens, top, experts, hidden, intermediate, v->permuted_rows) ? 1 : 0;
     v->hidden_q = take(tokens * hidden);
-    v->hidden_s = take(tokens * (hidden / 32));
+    v->hidden_s = take((v->route_scales ? v->permuted_rows : tokens) * (hidden / 32));
     v->gated_q = take(v->permuted_rows * intermediate);
     v->gated_s = take(v->permuted_rows * (intermediate / 32));
     v->hidden_route_s = -1;
@@ -108,12 +111,15 @@ namespace {
 template <class Want>
 int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_layer_views &v, char *ws,
                         const Want &want, void *stream) {
+  using namespace uniserve;
   auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
   const auto *t2e = static_cast<const int32_t *>(at(v.tile_to_expert));
   const auto *t2l = static_cast<const int32_t *>(at(v.tile_to_limit));
   const auto *p2e = static_cast<const int32_t *>(at(v.permuted_to_expanded));
   const auto *tiles = static_cast<const int32_t *>(at(v.num_non_exiting_tiles));
 
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t scale_rows = v.route_scales ? v.permuted_rows : 0;
   uniserve_quantize_mxfp8_call qx{};
   qx.input = call->hidden;
   qx.out = at(v.hidden_q);
@@ -121,8 +127,16 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   qx.rows = call->tokens;
   qx.width = call->hidden_size;
   qx.input_dtype = UNISERVE_DTYPE_BF16;
-  if (want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) && uniserve_quantize_mxfp8(&qx, stream) != 0)
+  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN)) {
+  } else if (scale_rows != 0) {
+    // Each token's scale words go to its routes' permuted rows.
+    launch_quantize_mxfp8(call->hidden, false, static_cast<uint8_t *>(at(v.hidden_q)), nullptr, nullptr, call->tokens,
+                          call->hidden_size, s, static_cast<uint8_t *>(at(v.hidden_s)),
+                          static_cast<const int32_t *>(at(v.expanded_to_permuted)), call->top, scale_rows);
+    if (int32_t status = launched(call, "quantize_mxfp8")) return status;
+  } else if (uniserve_quantize_mxfp8(&qx, stream) != 0) {
     return forward_error(call, "quantize_mxfp8", qx);
+  }
 
   // The call's scale pointers carry E8M0 bytes for MXFP4 stacks.
   uniserve_gather_mx_call fc1{};
@@ -143,7 +157,8 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   fc1.top = call->top;
   fc1.out_dtype = UNISERVE_DTYPE_BF16;
   fc1.multiprocessors = call->multiprocessors;
-  if (want(UNISERVE_MOE_LAYER_GATHER) && uniserve_gather_gemm_mx(&fc1, stream) != 0)
+  fc1.weight_scale_layout = call->weight_scale_layout;
+  if (want(UNISERVE_MOE_LAYER_GATHER) && gather_gemm_mx(&fc1, scale_rows, stream) != 0)
     return forward_error(call, "gather_gemm_mx", fc1);
 
   uniserve_quantize_mxfp8_call qg{};
@@ -154,8 +169,15 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   qg.rows = v.permuted_rows;
   qg.width = call->intermediate;
   qg.input_dtype = UNISERVE_DTYPE_BF16;
-  if (want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) && uniserve_quantize_mxfp8(&qg, stream) != 0)
+  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_GATED)) {
+  } else if (scale_rows != 0) {
+    launch_quantize_mxfp8(at(v.gated), false, static_cast<uint8_t *>(at(v.gated_q)), nullptr, qg.row_limit,
+                          v.permuted_rows, call->intermediate, s, static_cast<uint8_t *>(at(v.gated_s)), nullptr, 0,
+                          scale_rows);
+    if (int32_t status = launched(call, "quantize_mxfp8")) return status;
+  } else if (uniserve_quantize_mxfp8(&qg, stream) != 0) {
     return forward_error(call, "quantize_mxfp8", qg);
+  }
 
   uniserve_route_mx_call fc2{};
   fc2.rows = at(v.gated_q);
@@ -173,7 +195,8 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   fc2.experts = call->experts;
   fc2.out_dtype = UNISERVE_DTYPE_BF16;
   fc2.multiprocessors = call->multiprocessors;
-  if (want(UNISERVE_MOE_LAYER_ROUTE) && uniserve_route_gemm_mx(&fc2, stream) != 0)
+  fc2.weight_scale_layout = call->weight_scale_layout;
+  if (want(UNISERVE_MOE_LAYER_ROUTE) && route_gemm_mx(&fc2, scale_rows, stream) != 0)
     return forward_error(call, "route_gemm_mx", fc2);
   return 0;
 }
@@ -190,6 +213,9 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     const bool mx = call->weight_dtype == UNISERVE_DTYPE_F4E2M1;
     if ((fp8 || mx) && (call->up_gate_scales == nullptr || call->down_scales == nullptr))
       return UNISERVE_REFUSE(call, "moe_layer: quantised stacks need their block scales");
+    if (mx && call->weight_scale_layout != UNISERVE_MX_SCALES_ROW_MAJOR &&
+        call->weight_scale_layout != UNISERVE_MX_SCALES_STAGE_MAJOR)
+      return UNISERVE_REFUSE(call, "moe_layer: no MX scale layout %lld", static_cast<long long>(call->weight_scale_layout));
     if (mx && (call->hidden_size % 256 != 0 || call->intermediate % 256 != 0))
       return UNISERVE_REFUSE(call, "moe_layer: MXFP4 stacks need hidden and intermediate sizes of whole 256-element chunks");
     if (reinterpret_cast<uintptr_t>(call->workspace) % kAlign != 0)

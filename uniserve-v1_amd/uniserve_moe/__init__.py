@@ -15,6 +15,7 @@ from .abi import (  # noqa: F401
     LayerCall,
     LayerViews,
     QuantizeFp8Call,
+    MxStageScalesCall,
     QuantizeMxfp8Call,
     GatherMxCall,
     RouteMxCall,

@@ -244,6 +244,7 @@ class GatherMxCall(ctypes.Structure):
         ("top", _I64),
         ("out_dtype", _I64),
         ("multiprocessors", _I64),
+        ("weight_scale_layout", _I64),
         ("error", _ERR),
     ]
 
@@ -267,6 +268,20 @@ class RouteMxCall(ctypes.Structure):
         ("experts", _I64),
         ("out_dtype", _I64),
         ("multiprocessors", _I64),
+        ("weight_scale_layout", _I64),
+        ("error", _ERR),
+    ]
+
+
+class MxStageScalesCall(ctypes.Structure):
+    """``uniserve_mx_stage_scales_call``."""
+
+    _fields_ = [
+        ("input", _P),
+        ("out", _P),
+        ("stacks", _I64),
+        ("rows", _I64),
+        ("width", _I64),
         ("error", _ERR),
     ]
 
@@ -294,6 +309,7 @@ class LayerCall(ctypes.Structure):
         ("renormalize", _I64),
         ("weight_dtype", _I64),
         ("multiprocessors", _I64),
+        ("weight_scale_layout", _I64),
         ("error", _ERR),
     ]
 
@@ -370,6 +386,7 @@ _ENTRIES = {
     "uniserve_quantize_mxfp8": QuantizeMxfp8Call,
     "uniserve_gather_gemm_mx": GatherMxCall,
     "uniserve_route_gemm_mx": RouteMxCall,
+    "uniserve_mx_stage_major_scales": MxStageScalesCall,
 }
 
 

@@ -20,6 +20,7 @@ from .abi import (
     LayerCall,
     LayerViews,
     QuantizeFp8Call,
+    MxStageScalesCall,
     QuantizeMxfp8Call,
     GatherMxCall,
     RouteMxCall,
@@ -271,8 +272,25 @@ def quantize_mxfp8(rows_tensor, row_limit=None):
     return out, scales
 
 
-def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None):
-    """FC1 over MXFP8 tokens and MXFP4 weights (``up_gate_q`` [E, 2I, H / 2] E2M1 pairs)."""
+MX_SCALE_LAYOUTS = {"row": 0, "stage": 1}
+
+
+def mx_stage_major_scales(scales):
+    """A ``[stacks, rows, K / 32]`` row-major E8M0 table in the stage-major layout (same bytes,
+    each 128-element stage's 4-byte words of all rows contiguous), for the prefill kernel."""
+    stacks, rows, blocks = scales.shape
+    out = torch.empty_like(scales)
+    call = MxStageScalesCall()
+    call.input, call.out = scales.data_ptr(), out.data_ptr()
+    call.stacks, call.rows, call.width = stacks, rows, blocks * 32
+    _check(library().uniserve_mx_stage_major_scales(ctypes.byref(call), _stream(scales.device)), call,
+           "mx_stage_major_scales")
+    return out
+
+
+def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None, scale_layout="row"):
+    """FC1 over MXFP8 tokens and MXFP4 weights (``up_gate_q`` [E, 2I, H / 2] E2M1 pairs; the weight
+    scales in ``scale_layout``, "row" or "stage")."""
     tokens, width = hidden_q.shape
     experts, gated, _ = up_gate_q.shape
     if out is None:
@@ -287,12 +305,14 @@ def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, ou
     call.tokens, call.permuted_rows, call.width, call.hidden_size = tokens, rows, gated, width
     call.experts, call.top = experts, top
     call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(hidden_q.device)
+    call.weight_scale_layout = MX_SCALE_LAYOUTS[scale_layout]
     _check(library().uniserve_gather_gemm_mx(ctypes.byref(call), _stream(hidden_q.device)), call, "gather_gemm_mx")
     return out
 
 
-def route_gemm_mx(gated_q, gated_s, down_q, down_s, maps, out=None):
-    """FC2 over MXFP8 rows and MXFP4 weights (``down_q`` [E, H, I / 2] E2M1 pairs)."""
+def route_gemm_mx(gated_q, gated_s, down_q, down_s, maps, out=None, scale_layout="row"):
+    """FC2 over MXFP8 rows and MXFP4 weights (``down_q`` [E, H, I / 2] E2M1 pairs; the weight scales
+    in ``scale_layout``)."""
     rows, intermediate = gated_q.shape
     experts, hidden, _ = down_q.shape
     if out is None:
@@ -307,6 +327,7 @@ def route_gemm_mx(gated_q, gated_s, down_q, down_s, maps, out=None):
     call.permuted_rows, call.width, call.intermediate = rows, hidden, intermediate
     call.experts = experts
     call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(gated_q.device)
+    call.weight_scale_layout = MX_SCALE_LAYOUTS[scale_layout]
     _check(library().uniserve_route_gemm_mx(ctypes.byref(call), _stream(gated_q.device)), call, "route_gemm_mx")
     return out
 
@@ -343,7 +364,7 @@ class MoeLayer:
         return self.workspace[offset:offset + count * size].view(dtype).view(*shape)
 
     def __call__(self, hidden, router, up_gate, down, out=None, up_gate_scales=None, down_scales=None,
-                 router_bias=None, live_tokens=None):
+                 router_bias=None, live_tokens=None, scale_layout="row"):
         tokens = hidden.shape[0]
         if tokens != self.max_tokens:
             raise ValueError("the layer's workspace is laid out for its max_tokens")
@@ -361,6 +382,7 @@ class MoeLayer:
         call.renormalize = 1 if self.renormalize else 0
         call.weight_dtype = DTYPE[self.weight_dtype]
         call.multiprocessors = multiprocessors(hidden.device)
+        call.weight_scale_layout = MX_SCALE_LAYOUTS[scale_layout]
         _check(library().uniserve_moe_layer(ctypes.byref(call), _stream(hidden.device)), call, "moe_layer")
         return out
 
