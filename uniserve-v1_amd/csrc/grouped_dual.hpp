@@ -62,8 +62,14 @@ __device__ __forceinline__ intx8 fragment(const u32x4 *rows, int row, int g) {
                static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
 }
 
-template <bool kGated>
+/// kQuantize (FC1 only): the workgroup covers 128 output columns in two sweeps of 64 through one
+/// continuous stage pipeline (the first sweep's gated values parked in registers as bf16), and
+/// writes them as FC2's e4m3 operand - codes and one scale per 128 columns, the rounding points
+/// and encoding of uniserve_quantize_fp8 over the bf16 values.
+template <bool kGated, bool kQuantize>
 __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
+  static_assert(kGated || !kQuantize, "only FC1 quantises its output");
+  constexpr int kSweeps = kQuantize ? 2 : 1;
   using prefill::dma16;
   using prefill::lds_address;
   __shared__ Stage ring[2];
@@ -113,7 +119,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   // instruction brings the scales of tile rows 32 w + l % 32 (lanes 32.. repeat them into the
   // padding). Slice row j is, for FC1, up row slice_col + j (j < 64) or gate row out_width +
   // slice_col + j - 64; for FC2, row slice_col + j.
-  const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSliceRows / 2 : kSliceRows);
+  const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSweeps * kSliceRows / 2 : kSliceRows);
   auto weight_row = [&](int j) -> int64_t {
     if constexpr (kGated) return j < 64 ? slice_col + j : p.out_width + slice_col + j - 64;
     else return slice_col + j;
@@ -151,7 +157,11 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   float s_first_k = __int_as_float(__builtin_amdgcn_readlane(sw_first_lanes, 0));
   float s_second_k = __int_as_float(__builtin_amdgcn_readlane(sw_second_lanes, 0));
 
-  auto issue = [&](Stage &st, int k) {
+  // Virtual stage v: sweep v / stages (its weight rows 64 columns on), K stage v % stages.
+  auto issue = [&](Stage &st, int v) {
+    const int sweep = kSweeps == 1 ? 0 : v / stages;
+    const int k = v - sweep * stages;
+    const uint8_t *sweep_weights = expert_weights + static_cast<int64_t>(sweep) * 64 * p.K;
     const uint32_t act_lds = lds_address(st.act + wave * 4 * kWave);
     const uint32_t weight_lds = lds_address(st.weights + wave * 4 * kWave);
 #pragma unroll
@@ -159,7 +169,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
       dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dma16(expert_weights + static_cast<int64_t>(w_first[i]) * p.K + static_cast<int64_t>(k) * 128, w_lane[i & 1],
+      dma16(sweep_weights + static_cast<int64_t>(w_first[i]) * p.K + static_cast<int64_t>(k) * 128, w_lane[i & 1],
             __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
     dma4(reinterpret_cast<const uint8_t *>(p.act_scales) + k * as_stage, as_off,
          __builtin_amdgcn_readfirstlane(lds_address(st.act_scales + wave * kWave)));
@@ -217,12 +227,31 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   // wave (own wait, then the barrier, which also retires every wave's reads of stage k - 1), stage
   // k + 1 is issued into the other buffer. The issue past the last stage re-reads it, so every wait
   // counts the same loads. ----
+  // The first sweep's gated values (FC1 with kQuantize), bf16 pairs: token block tb, up block jb.
+  uint2 parked[4][2];
+  const int total = kSweeps * stages;
   issue(ring[0], 0);
-  for (int k = 0; k < stages; ++k) {
+  for (int v = 0; v < total; ++v) {
     prefill::wait_all_loads();
     __syncthreads();
-    issue(ring[(k + 1) & 1], min(k + 1, stages - 1));
-    compute(ring[k & 1], k);
+    issue(ring[(v + 1) & 1], min(v + 1, total - 1));
+    const int k = kSweeps == 1 ? v : v % stages;
+    compute(ring[v & 1], k);
+    if constexpr (kQuantize) {
+      if (v == stages - 1) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb) {
+            float g4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) g4[i] = silu(acc[tb][jb + 2][i]) * acc[tb][jb][i];
+            parked[tb][jb] = uint2{pack_bf16x2(g4[0], g4[1]), pack_bf16x2(g4[2], g4[3])};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tb][jb][i] = acc[tb][jb + 2][i] = 0.0f;
+          }
+      }
+    }
   }
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done reading the stage buffers
@@ -230,7 +259,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row
   // 64 t + 16 tb + r16 and the block's rows 4 g + i in element i. The output tile goes through LDS
   // so the global stores are whole rows; LDS rows are padded by 16 bytes. ----
-  constexpr int kOutCols = kGated ? kSliceRows / 2 : kSliceRows;
+  constexpr int kOutCols = kGated ? kSweeps * kSliceRows / 2 : kSliceRows;
   constexpr int kOutStride = kOutCols * 2 + 16;
   static_assert(kRows * kOutStride <= static_cast<int>(sizeof(ring)), "the output tile fits the stages");
   char *tile_lds = reinterpret_cast<char *>(ring);
@@ -246,7 +275,8 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
         uint2 packed;
         packed.x = pack_bf16x2(v[0], v[1]);
         packed.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2 *>(row + (ww * 32 + jb * 16 + 4 * g) * 2) = packed;
+        *reinterpret_cast<uint2 *>(row + ((kSweeps - 1) * 64 + ww * 32 + jb * 16 + 4 * g) * 2) = packed;
+        if constexpr (kQuantize) *reinterpret_cast<uint2 *>(row + (ww * 32 + jb * 16 + 4 * g) * 2) = parked[tb][jb];
       }
     } else {
 #pragma unroll
@@ -259,6 +289,35 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
     }
   }
   __syncthreads();
+  if constexpr (kQuantize) {
+    // Each row's 128 columns are quantised by 16 lanes from the bf16 values in LDS: amax of the
+    // bf16 values, s = amax / 448 (1 for an all-zero group), code = e4m3(v / s); live rows only.
+    const int sub = t & 15;
+    const int64_t groups_per_row = p.out_width / 128;
+    for (int m = t / 16; m < kRows; m += kThreads / 16) {
+      const u32x4 piece = *reinterpret_cast<const u32x4 *>(tile_lds + m * kOutStride + sub * 16);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(piece[j] << 16);
+        v[2 * j + 1] = __uint_as_float(piece[j] & 0xffff0000u);
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+#pragma unroll
+      for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+      if (m >= rows) continue;
+      const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + slice_col + sub * 8) = e4m3_eight(v, scale);
+      if (sub == 0) {
+        const int64_t at = p.scale_rows != 0 ? slice_col / 128 * p.scale_rows + first + m
+                                             : (first + m) * groups_per_row + slice_col / 128;
+        p.out_code_scales[at] = scale;
+      }
+    }
+    return;
+  }
   constexpr int kPieces = kOutCols / 8;
   for (int index = t; index < kRows * kPieces; index += kThreads) {
     const int m = index / kPieces;
@@ -272,22 +331,24 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
 }  // namespace dual
 
 /// Whether the dual-workgroup e4m3 kernel serves the shape: whole 128-K stages (at most 64 of
-/// them), whole 64-column (FC1) or 128-column (FC2) slices, bf16 output.
-inline bool dual_fits(bool gated, int64_t K, int64_t out_width) {
+/// them), whole 64-column (FC1), 128-column (FC1 writing e4m3 codes) or 128-column (FC2) slices.
+inline bool dual_fits(bool gated, int64_t K, int64_t out_width, bool quantize = false) {
   return K % 128 == 0 && K > 0 && K / 128 <= kWave &&
-         out_width % (gated ? dual::kSliceRows / 2 : dual::kSliceRows) == 0;
+         out_width % (gated && !quantize ? dual::kSliceRows / 2 : dual::kSliceRows) == 0;
 }
 
 /// Launches the dual-workgroup e4m3 product over `max_tiles` tiles (tiles past `num_tiles` exit at
-/// once); `p.out_codes` must be null.
+/// once); with `p.out_codes` set (FC1 only) the gated rows are written as e4m3 codes and scales.
 inline void launch_dual_e4m3(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream, int group = 16) {
-  p.slices = static_cast<int32_t>(p.out_width / (gated ? dual::kSliceRows / 2 : dual::kSliceRows));
+  const bool quantize = gated && p.out_codes != nullptr;
+  p.slices = static_cast<int32_t>(p.out_width / (gated && !quantize ? dual::kSliceRows / 2 : dual::kSliceRows));
   p.max_tiles = static_cast<int32_t>(max_tiles);
   p.group = group;
   p.groups_per_xcd = static_cast<int32_t>(ceil_div<int64_t>(ceil_div<int64_t>(max_tiles, group), 8));
-  const int64_t blocks = static_cast<int64_t>(p.groups_per_xcd) * group * p.slices * 8;
-  if (gated) hipLaunchKernelGGL((dual::e4m3_kernel<true>), dim3(static_cast<uint32_t>(blocks)), dim3(dual::kThreads), 0, stream, p);
-  else hipLaunchKernelGGL((dual::e4m3_kernel<false>), dim3(static_cast<uint32_t>(blocks)), dim3(dual::kThreads), 0, stream, p);
+  const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(p.groups_per_xcd) * group * p.slices * 8));
+  if (quantize) hipLaunchKernelGGL((dual::e4m3_kernel<true, true>), grid, dim3(dual::kThreads), 0, stream, p);
+  else if (gated) hipLaunchKernelGGL((dual::e4m3_kernel<true, false>), grid, dim3(dual::kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((dual::e4m3_kernel<false, false>), grid, dim3(dual::kThreads), 0, stream, p);
 }
 
 }  // namespace uniserve

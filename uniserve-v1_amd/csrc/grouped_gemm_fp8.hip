@@ -470,7 +470,7 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
     q.scale_rows = p.scale_rows;
-    if (q.out_codes == nullptr && dual_fits(gated, q.K, q.out_width)) {
+    if (dual_fits(gated, q.K, q.out_width, q.out_codes != nullptr)) {
       launch_dual_e4m3(q, gated, max_tiles, stream);
       return;
     }
@@ -523,7 +523,8 @@ extern "C" int32_t uniserve_quantize_fp8(const uniserve_quantize_fp8_call *call,
 namespace uniserve {
 
 bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate) {
-  return !fp8_stream_path(tokens * top, experts) && prefill_fits<prefill::E4m3, true>(hidden_size, intermediate);
+  return !fp8_stream_path(tokens * top, experts) &&
+         (dual_fits(true, hidden_size, intermediate, true) || prefill_fits<prefill::E4m3, true>(hidden_size, intermediate));
 }
 
 bool fp8_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate,
