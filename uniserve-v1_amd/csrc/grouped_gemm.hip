@@ -70,8 +70,11 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
 
 // ---- stream kernel (decode) ----------------------------------------------------------------------------
 
-/// Rows of a tile one pass covers: kPassTiles MFMA blocks of 16.
-constexpr int kPassTiles = 2;
+/// Average routes per expert at or below which the stream kernel takes a tile in passes of one
+/// 16-row MFMA block instead of two: 150 instead of 192 VGPRs, three waves per SIMD instead of
+/// two (FC2 at 64-token decode 68 vs 71.5 us); a tile with more rows re-streams its weights per
+/// pass, which at such averages is rare.
+constexpr int64_t kOnePassRowsPerExpert = 8;
 
 //
 // Grid: (max tiles, weight-row slices). FC1 slices are 64 gated columns (64 up + 64 gate rows),
@@ -97,7 +100,8 @@ __device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
   return out;
 }
 
-template <bool kGated>
+/// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
+template <bool kGated, int kPassTiles>
 __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   const int tile = static_cast<int>(blockIdx.x);
   if (tile >= p.num_tiles[0]) return;
@@ -336,7 +340,7 @@ __global__ void __launch_bounds__(kThreads) tiled_kernel(GroupedParams p) {
 constexpr int64_t kStreamRowsPerExpert = 24;
 
 template <bool kGated>
-void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, hipStream_t s) {
+void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, bool one_pass, hipStream_t s) {
   if (!stream_path && prefill_fits<prefill::Bf16, kGated>(p.K, p.out_width)) {
     PrefillParams q{};
     q.act = reinterpret_cast<const uint8_t *>(p.act);
@@ -355,7 +359,8 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
   }
   const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);
   const dim3 grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(slices));
-  if (stream_path) hipLaunchKernelGGL(stream_kernel<kGated>, grid, dim3(kThreads), 0, s, p);
+  if (stream_path && one_pass) hipLaunchKernelGGL((stream_kernel<kGated, 1>), grid, dim3(kThreads), 0, s, p);
+  else if (stream_path) hipLaunchKernelGGL((stream_kernel<kGated, 2>), grid, dim3(kThreads), 0, s, p);
   else hipLaunchKernelGGL(tiled_kernel<kGated>, grid, dim3(kThreads), 0, s, p);
 }
 
@@ -406,7 +411,8 @@ extern "C" int32_t uniserve_gather_gemm(const uniserve_gather_call *call, void *
     p.top = call->top;
     const bool stream_path = call->tokens * call->top < kStreamRowsPerExpert * call->experts &&
                              call->hidden_size % 128 == 0;
-    launch_grouped<true>(p, max_tiles, stream_path, static_cast<hipStream_t>(stream));
+    launch_grouped<true>(p, max_tiles, stream_path, call->tokens * call->top <= kOnePassRowsPerExpert * call->experts,
+                         static_cast<hipStream_t>(stream));
     return launched(call, "gather_gemm");
   });
 }
@@ -450,7 +456,8 @@ extern "C" int32_t uniserve_route_gemm(const uniserve_route_call *call, void *st
     const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
     const bool stream_path = routes_bound < kStreamRowsPerExpert * call->experts &&
                              call->intermediate % 128 == 0;
-    launch_grouped<false>(p, max_tiles, stream_path, static_cast<hipStream_t>(stream));
+    launch_grouped<false>(p, max_tiles, stream_path, routes_bound <= kOnePassRowsPerExpert * call->experts,
+                          static_cast<hipStream_t>(stream));
     return launched(call, "route_gemm");
   });
 }
