@@ -75,7 +75,7 @@ struct GroupedFp8Params {
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
                          const int32_t *row_limit, int64_t rows, int64_t width, hipStream_t stream);
-void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
+void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream);
 bool fp8_stream_path(int64_t routes, int64_t experts);
 

@@ -99,7 +99,10 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
   *reinterpret_cast<uint2 *>(pointer) = packed;
 }
 
-constexpr int kPassTiles = 2;
+/// Average routes per expert at or below which the stream kernel takes a tile in passes of one
+/// 16-row MFMA block instead of two (fewer registers, more waves per SIMD; a tile with more rows
+/// re-streams its weights per pass, which at such averages is rare).
+constexpr int64_t kOnePassRowsPerExpert = 8;
 
 /// The 16 bytes lane `source` holds in `value`, gathered by this lane (ds_bpermute: lanes exchange
 /// registers without LDS allocation).
@@ -116,7 +119,8 @@ constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is spli
 /// wavefronts share one row set and split K (scale block kb goes to wave kb % 4), their partial sums
 /// meeting in LDS in wave order - four times the workgroups, for batches whose tiles x slices would
 /// leave most of the chip idle (a single token: 8 tiles).
-template <bool kGated, bool kSplit>
+/// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
+template <bool kGated, bool kSplit, int kPassTiles>
 __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p) {
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   const int tile = static_cast<int>(blockIdx.x);
@@ -448,7 +452,7 @@ void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scal
   hipLaunchKernelGGL(quantize_kernel, dim3(quantize_blocks(rows, width)), dim3(kQuantThreads), 0, stream, p);
 }
 
-void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path,
+void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream) {
   const bool fits = gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
                           : prefill_fits<prefill::E4m3, false>(p.K, p.out_width);
@@ -485,12 +489,16 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     if (max_tiles * slices < kSplitBelow) {
       const int64_t split_slices = gated ? p.out_width / 16 : ceil_div<int64_t>(p.out_width, 32);
       const dim3 split_grid(static_cast<uint32_t>(max_tiles), static_cast<uint32_t>(split_slices));
-      if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, true>), split_grid, dim3(kThreads), 0, stream, p);
-      else hipLaunchKernelGGL((stream_fp8_kernel<false, true>), split_grid, dim3(kThreads), 0, stream, p);
+      if (gated && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 1>), split_grid, dim3(kThreads), 0, stream, p);
+      else if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 2>), split_grid, dim3(kThreads), 0, stream, p);
+      else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 1>), split_grid, dim3(kThreads), 0, stream, p);
+      else hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2>), split_grid, dim3(kThreads), 0, stream, p);
     } else if (gated) {
-      hipLaunchKernelGGL((stream_fp8_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
+      if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, false, 1>), grid, dim3(kThreads), 0, stream, p);
+      else hipLaunchKernelGGL((stream_fp8_kernel<true, false, 2>), grid, dim3(kThreads), 0, stream, p);
     } else {
-      hipLaunchKernelGGL((stream_fp8_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+      if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, false, 1>), grid, dim3(kThreads), 0, stream, p);
+      else hipLaunchKernelGGL((stream_fp8_kernel<false, false, 2>), grid, dim3(kThreads), 0, stream, p);
     }
   } else {
     if (gated) hipLaunchKernelGGL(tiled_fp8_kernel<true>, grid, dim3(kThreads), 0, stream, p);
@@ -583,6 +591,7 @@ int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, fl
       p.scale_rows = scale_rows;
     }
     launch_grouped_fp8(p, true, max_tiles, fp8_stream_path(call->tokens * call->top, call->experts),
+                       call->tokens * call->top <= kOnePassRowsPerExpert * call->experts,
                        static_cast<hipStream_t>(stream));
     return launched(call, "gather_gemm_fp8");
   });
@@ -642,7 +651,8 @@ int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, 
         return UNISERVE_REFUSE(call, "route_gemm_fp8 takes route-major scales only on the prefill kernel's shapes");
       p.scale_rows = scale_rows;
     }
-    launch_grouped_fp8(p, false, max_tiles, stream_path, static_cast<hipStream_t>(stream));
+    launch_grouped_fp8(p, false, max_tiles, stream_path, routes_bound <= kOnePassRowsPerExpert * call->experts,
+                       static_cast<hipStream_t>(stream));
     return launched(call, "route_gemm_fp8");
   });
 }
