@@ -14,7 +14,9 @@
 namespace uniserve {
 namespace {
 
-constexpr int kCombineThreads = 128;
+// 256 lanes (a 2048-wide bf16 row per workgroup) and non-temporal route loads - every route row is
+// read once: 49 us for 8192 tokens x 8 routes x 2048, against 65 with 128 lanes and plain loads.
+constexpr int kCombineThreads = 256;
 constexpr int kPerLane = 8;
 constexpr int kColumnsPerBlock = kCombineThreads * kPerLane;
 
@@ -75,7 +77,12 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
     for (int u = 0; u < kBatch; ++u) {
       const bool visible = entry[u] >= 0 && entry[u] < p.routes_rows;
       const int64_t row = p.expanded ? token * p.top + k0 + u : entry[u];
-      packed[u] = visible ? *reinterpret_cast<const uint4 *>(routes + row * p.hidden + column) : uint4{0, 0, 0, 0};
+      if (visible) {
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(routes + row * p.hidden + column));
+        packed[u] = uint4{v[0], v[1], v[2], v[3]};
+      } else {
+        packed[u] = uint4{0, 0, 0, 0};
+      }
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
