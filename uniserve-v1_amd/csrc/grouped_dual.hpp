@@ -62,14 +62,16 @@ __device__ __forceinline__ intx8 fragment(const u32x4 *rows, int row, int g) {
                static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
 }
 
-/// kQuantize (FC1 only): the workgroup covers 128 output columns in two sweeps of 64 through one
-/// continuous stage pipeline (the first sweep's gated values parked in registers as bf16), and
-/// writes them as FC2's e4m3 operand - codes and one scale per 128 columns, the rounding points
-/// and encoding of uniserve_quantize_fp8 over the bf16 values.
+/// A workgroup covers its columns in sweeps through one continuous stage pipeline, each sweep's
+/// results but the last parked in registers as bf16: FC1 64 columns (one sweep), or with kQuantize
+/// 128 columns in two sweeps of 64, written as FC2's e4m3 operand - codes and one scale per 128
+/// columns, the rounding points and encoding of uniserve_quantize_fp8 over the bf16 values; FC2 256
+/// columns in two sweeps of 128, which halves the per-item prologue and epilogue of its short K.
 template <bool kGated, bool kQuantize>
 __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   static_assert(kGated || !kQuantize, "only FC1 quantises its output");
-  constexpr int kSweeps = kQuantize ? 2 : 1;
+  constexpr int kSweeps = (kQuantize || !kGated) ? 2 : 1;
+  constexpr int kSweepCols = kGated ? kSliceRows / 2 : kSliceRows;  // output columns per sweep
   using prefill::dma16;
   using prefill::lds_address;
   __shared__ Stage ring[2];
@@ -119,7 +121,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   // instruction brings the scales of tile rows 32 w + l % 32 (lanes 32.. repeat them into the
   // padding). Slice row j is, for FC1, up row slice_col + j (j < 64) or gate row out_width +
   // slice_col + j - 64; for FC2, row slice_col + j.
-  const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSweeps * kSliceRows / 2 : kSliceRows);
+  const int64_t slice_col = static_cast<int64_t>(slice) * kSweeps * kSweepCols;
   auto weight_row = [&](int j) -> int64_t {
     if constexpr (kGated) return j < 64 ? slice_col + j : p.out_width + slice_col + j - 64;
     else return slice_col + j;
@@ -144,12 +146,15 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   const uint32_t as_off = p.scale_rows != 0 ? static_cast<uint32_t>((first + (scale_r < rows ? scale_r : 0)) * 4)
                                             : static_cast<uint32_t>(source_row(scale_r) * kb_count * 4);
   const int64_t as_stage = p.scale_rows != 0 ? p.scale_rows * 4 : 4;
-  // Weight block scales ([experts, n_total / 128, K / 128]): the wave's up and gate blocks (FC1) or
-  // its one block (FC2), wave-uniform. Lane k holds stage k's (K / 128 <= 64), read into a scalar
-  // per stage, so the loop issues no vector loads of its own besides the counted DMA.
+  // Weight block scales ([experts, n_total / 128, K / 128]): the wave's up and gate blocks (FC1; the
+  // same for both sweeps, which share one 128-column block) or its blocks of sweeps 0 and 1 (FC2),
+  // wave-uniform. Lane k holds stage k's (K / 128 <= 64), read into a scalar per stage, so the loop
+  // issues no vector loads of its own besides the counted DMA.
   const int64_t blocks_n = p.n_total / 128;
-  const float *sw_first = p.weight_scales + (expert * blocks_n + weight_row(kGated ? 0 : 64 * ww) / 128) * kb_count;
-  const float *sw_second = p.weight_scales + (expert * blocks_n + weight_row(kGated ? 64 : 64 * ww) / 128) * kb_count;
+  const float *sw_first =
+      p.weight_scales + (expert * blocks_n + weight_row(kGated ? 0 : 64 * ww) / 128) * kb_count;
+  const float *sw_second =
+      p.weight_scales + (expert * blocks_n + (kGated ? weight_row(64) : weight_row(64 * ww) + kSweepCols) / 128) * kb_count;
   const int sw_lane = lane < stages ? lane : 0;
   const int sw_first_lanes = __float_as_int(sw_first[sw_lane]);
   const int sw_second_lanes = __float_as_int(sw_second[sw_lane]);
@@ -157,11 +162,11 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   float s_first_k = __int_as_float(__builtin_amdgcn_readlane(sw_first_lanes, 0));
   float s_second_k = __int_as_float(__builtin_amdgcn_readlane(sw_second_lanes, 0));
 
-  // Virtual stage v: sweep v / stages (its weight rows 64 columns on), K stage v % stages.
+  // Virtual stage v: sweep v / stages (its weight rows kSweepCols columns on), K stage v % stages.
   auto issue = [&](Stage &st, int v) {
     const int sweep = kSweeps == 1 ? 0 : v / stages;
     const int k = v - sweep * stages;
-    const uint8_t *sweep_weights = expert_weights + static_cast<int64_t>(sweep) * 64 * p.K;
+    const uint8_t *sweep_weights = expert_weights + static_cast<int64_t>(sweep) * kSweepCols * p.K;
     const uint32_t act_lds = lds_address(st.act + wave * 4 * kWave);
     const uint32_t weight_lds = lds_address(st.weights + wave * 4 * kWave);
 #pragma unroll
@@ -187,7 +192,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
     if constexpr (kGated) return (jb >> 1) * 64 + ww * 32 + (jb & 1) * 16 + r16;
     else return ww * 64 + jb * 16 + r16;
   };
-  auto compute = [&](const Stage &st, int k) {
+  auto compute = [&](const Stage &st, int k, int sweep) {
     const float s_first = k == 0 ? s_first_k : __int_as_float(__builtin_amdgcn_readlane(sw_first_lanes, k));
     const float s_second = k == 0 ? s_second_k : __int_as_float(__builtin_amdgcn_readlane(sw_second_lanes, k));
     intx8 wf[4];
@@ -215,7 +220,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
         const int pb = (tb - 1) & 1;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
-          const float s = scale[pb][kGated ? (jb >> 1) : 0];
+          const float s = scale[pb][kGated ? (jb >> 1) : sweep];
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[tb - 1][jb][e] = __builtin_fmaf(block[pb][jb][e], s, acc[tb - 1][jb][e]);
         }
@@ -227,16 +232,28 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   // wave (own wait, then the barrier, which also retires every wave's reads of stage k - 1), stage
   // k + 1 is issued into the other buffer. The issue past the last stage re-reads it, so every wait
   // counts the same loads. ----
-  // The first sweep's gated values (FC1 with kQuantize), bf16 pairs: token block tb, up block jb.
-  uint2 parked[4][2];
+  // The first sweep's results, bf16: token block tb, weight block jb (FC1: up blocks 0, 1).
+  uint2 parked[4][4];
   const int total = kSweeps * stages;
   issue(ring[0], 0);
   for (int v = 0; v < total; ++v) {
     prefill::wait_all_loads();
     __syncthreads();
     issue(ring[(v + 1) & 1], min(v + 1, total - 1));
-    const int k = kSweeps == 1 ? v : v % stages;
-    compute(ring[v & 1], k);
+    const int sweep = kSweeps == 1 ? 0 : v / stages;
+    compute(ring[v & 1], v - sweep * stages, sweep);
+    if constexpr (!kGated) {
+      if (v == stages - 1) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) {
+            parked[tb][jb] = uint2{pack_bf16x2(acc[tb][jb][0], acc[tb][jb][1]), pack_bf16x2(acc[tb][jb][2], acc[tb][jb][3])};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tb][jb][i] = 0.0f;
+          }
+      }
+    }
     if constexpr (kQuantize) {
       if (v == stages - 1) {
 #pragma unroll
@@ -259,7 +276,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
   // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row
   // 64 t + 16 tb + r16 and the block's rows 4 g + i in element i. The output tile goes through LDS
   // so the global stores are whole rows; LDS rows are padded by 16 bytes. ----
-  constexpr int kOutCols = kGated ? kSweeps * kSliceRows / 2 : kSliceRows;
+  constexpr int kOutCols = kSweeps * kSweepCols;
   constexpr int kOutStride = kOutCols * 2 + 16;
   static_assert(kRows * kOutStride <= static_cast<int>(sizeof(ring)), "the output tile fits the stages");
   char *tile_lds = reinterpret_cast<char *>(ring);
@@ -284,7 +301,8 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
         uint2 packed;
         packed.x = pack_bf16x2(acc[tb][jb][0], acc[tb][jb][1]);
         packed.y = pack_bf16x2(acc[tb][jb][2], acc[tb][jb][3]);
-        *reinterpret_cast<uint2 *>(row + (ww * 64 + jb * 16 + 4 * g) * 2) = packed;
+        *reinterpret_cast<uint2 *>(row + (kSweepCols + ww * 64 + jb * 16 + 4 * g) * 2) = packed;
+        *reinterpret_cast<uint2 *>(row + (ww * 64 + jb * 16 + 4 * g) * 2) = parked[tb][jb];
       }
     }
   }
@@ -330,18 +348,20 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
 
 }  // namespace dual
 
+/// Output columns per workgroup: FC1 64, FC1 writing e4m3 codes 128, FC2 256.
+inline int64_t dual_columns(bool gated, bool quantize) { return gated ? (quantize ? 128 : 64) : 256; }
+
 /// Whether the dual-workgroup e4m3 kernel serves the shape: whole 128-K stages (at most 64 of
-/// them), whole 64-column (FC1), 128-column (FC1 writing e4m3 codes) or 128-column (FC2) slices.
+/// them) and whole slices of dual_columns.
 inline bool dual_fits(bool gated, int64_t K, int64_t out_width, bool quantize = false) {
-  return K % 128 == 0 && K > 0 && K / 128 <= kWave &&
-         out_width % (gated && !quantize ? dual::kSliceRows / 2 : dual::kSliceRows) == 0;
+  return K % 128 == 0 && K > 0 && K / 128 <= kWave && out_width % dual_columns(gated, quantize) == 0;
 }
 
 /// Launches the dual-workgroup e4m3 product over `max_tiles` tiles (tiles past `num_tiles` exit at
 /// once); with `p.out_codes` set (FC1 only) the gated rows are written as e4m3 codes and scales.
 inline void launch_dual_e4m3(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream, int group = 16) {
   const bool quantize = gated && p.out_codes != nullptr;
-  p.slices = static_cast<int32_t>(p.out_width / (gated && !quantize ? dual::kSliceRows / 2 : dual::kSliceRows));
+  p.slices = static_cast<int32_t>(p.out_width / dual_columns(gated, quantize));
   p.max_tiles = static_cast<int32_t>(max_tiles);
   p.group = group;
   p.groups_per_xcd = static_cast<int32_t>(ceil_div<int64_t>(ceil_div<int64_t>(max_tiles, group), 8));
