@@ -65,7 +65,9 @@ def test_stage_major_scales_are_the_row_major_bytes_regrouped(device):
 @pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew,layout", [
     (64, 2048, 128, 8, 768, "uniform", "row"), (1, 4096, 128, 8, 1536, "uniform", "row"),
     (512, 2048, 128, 8, 768, "zipf", "row"), (1024, 4096, 128, 8, 1536, "zipf", "row"),
-    (64, 2048, 128, 8, 768, "uniform", "stage"), (512, 2048, 128, 8, 768, "zipf", "stage")])
+    (64, 2048, 128, 8, 768, "uniform", "stage"), (512, 2048, 128, 8, 768, "zipf", "stage"),
+    # the tiled kernel at its smallest shapes: two K stages, one weight slice, ragged tiles
+    (600, 256, 8, 2, 256, "zipf", "row")])
 def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew, layout):
     announce("mx products", tokens, hidden, experts, top, intermediate, skew, layout)
     rng = np.random.default_rng(tokens + 7)
