@@ -296,3 +296,48 @@ def test_layer_steps_replay_the_call(device, wdtype, tokens):
         layer.step(name)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(bf16_bits(out), want)
+
+
+@pytest.mark.parametrize("wdtype,tokens", [("bf16", 64), ("f8e4m3", 2048)])
+def test_layer_is_invariant_under_a_redistribution_of_the_experts(device, wdtype, tokens):
+    """crates/nn/tests/moe.rs:1071-1098: the experts stored in another order (router rows and both
+    stacks permuted alike) give the same routes and the same output. Experts whose bf16 scores tie
+    are picked lower index first, so a redistribution may pick another of equally scored experts
+    (checked: the picks that differ score the same) or swap two tied picks. The softmax sums its
+    exponentials in lane order, so moving the experts moves the FP32 rounding of the weights by an
+    ulp or two; a route's products do not depend on where its expert sits. So: weights within a few
+    FP32 ulps, outputs within one bf16 step of their token's peak, and nearly every element bit for bit."""
+    announce("layer redistribution", wdtype, tokens)
+    hidden, experts, top, intermediate = 2048, 128, 8, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 50)
+    args = {}
+    if wdtype == "f8e4m3":
+        q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+        up_gate, down = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+        args = dict(up_gate_scales=torch.from_numpy(s1).to(device), down_scales=torch.from_numpy(s2).to(device))
+    order = torch.from_numpy(np.random.default_rng(51).permutation(experts)).to(device)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+    first = bf16_bits(layer(x, router, up_gate, down, **args)).copy()
+    ids = layer.view("ids", torch.int32, (tokens, top)).cpu().numpy().copy()
+    scores = bf16_values(layer.view("scores", torch.bfloat16, (tokens, experts)))
+    weights = layer.view("weights", torch.float32, (tokens, top)).cpu().numpy().copy()
+    moved = {k: v[order].contiguous() for k, v in args.items()}
+    second = bf16_bits(layer(x, router[order].contiguous(), up_gate[order].contiguous(), down[order].contiguous(),
+                             **moved)).copy()
+    moved_ids = order.cpu().numpy()[layer.view("ids", torch.int32, (tokens, top)).cpu().numpy()]
+    same_set = (np.sort(moved_ids, axis=1) == np.sort(ids, axis=1)).all(axis=1)
+    for t in np.flatnonzero(~same_set):
+        gone = sorted(scores[t, e] for e in set(ids[t]) - set(moved_ids[t]))
+        came = sorted(scores[t, e] for e in set(moved_ids[t]) - set(ids[t]))
+        assert gone == came, (t, gone, came)
+    same = (moved_ids == ids).all(axis=1)
+    assert same.mean() > 0.5, "most tokens have no tied picks"
+    moved_weights = layer.view("weights", torch.float32, (tokens, top)).cpu().numpy()
+    np.testing.assert_allclose(moved_weights[same], weights[same], rtol=4 * 2.0 ** -23, atol=0)
+    assert (second[same] == first[same]).mean() > 0.999
+    a = O.bf16_decode(first[same_set]).astype(np.float64)
+    b = O.bf16_decode(second[same_set]).astype(np.float64)
+    # One bf16 step of the row's peak: a sum that nearly cancels has no relative bound per element.
+    peak = np.maximum(np.abs(a).max(axis=1, keepdims=True), np.abs(b).max(axis=1, keepdims=True))
+    assert (np.abs(a - b) <= 2.0 ** -7 * peak).all()
