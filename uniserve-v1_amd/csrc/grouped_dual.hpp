@@ -359,7 +359,8 @@ inline bool dual_fits(bool gated, int64_t K, int64_t out_width, bool quantize = 
 
 /// Launches the dual-workgroup e4m3 product over `max_tiles` tiles (tiles past `num_tiles` exit at
 /// once); with `p.out_codes` set (FC1 only) the gated rows are written as e4m3 codes and scales.
-inline void launch_dual_e4m3(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream, int group = 16) {
+/// `group`: tiles per group of the work numbering (4 measured best: 235B FC1 765 us against 792 at 16).
+inline void launch_dual_e4m3(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream, int group = 4) {
   const bool quantize = gated && p.out_codes != nullptr;
   p.slices = static_cast<int32_t>(p.out_width / dual_columns(gated, quantize));
   p.max_tiles = static_cast<int32_t>(max_tiles);
