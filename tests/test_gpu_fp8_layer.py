@@ -175,14 +175,28 @@ def sampled_layer(x_bits, ids, weights, host_w, experts, top):
     return O.bf16_decode(O.bf16_encode(combined)).astype(np.float64)
 
 
-def test_layer_live_tokens_leave_padding_rows_zero(device):
-    announce("layer live tokens")
+@pytest.mark.parametrize("wdtype", ["bf16", "f8e4m3", "f4e2m1"])
+def test_layer_live_tokens_leave_padding_rows_zero(device, wdtype):
+    """Rows past the live count come out zero and the live rows are the full call's, bit for bit
+    (their routes, products and combine do not see the dead rows), for every weight type."""
+    announce("layer live tokens", wdtype)
     tokens, hidden, experts, top, intermediate = 64, 2048, 128, 8, 768
     x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 10)
-    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens)
-    full = layer(x, router, up_gate, down).clone()
+    args = {}
+    if wdtype == "f8e4m3":
+        q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+        up_gate, down = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+        args = dict(up_gate_scales=torch.from_numpy(s1).to(device), down_scales=torch.from_numpy(s2).to(device))
+    elif wdtype == "f4e2m1":
+        q1, s1 = O.quantize_blocks_mxfp4(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_mxfp4(bf16_bits(down))
+        up_gate, down = torch.from_numpy(q1).to(device), torch.from_numpy(q2).to(device)
+        args = dict(up_gate_scales=torch.from_numpy(s1).to(device), down_scales=torch.from_numpy(s2).to(device))
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+    full = layer(x, router, up_gate, down, **args).clone()
     live = torch.tensor([40], dtype=torch.int32, device=device)
-    part = layer(x, router, up_gate, down, live_tokens=live)
+    part = layer(x, router, up_gate, down, live_tokens=live, **args)
     torch.cuda.synchronize()
     assert (bf16_values(part)[40:] == 0).all()
     np.testing.assert_array_equal(bf16_bits(part)[:40], bf16_bits(full)[:40])
