@@ -242,3 +242,18 @@ def test_own_structures_match_the_compiler(tmp_path):
         assert ctypes.sizeof(mirror) == measured[(struct, "size")], struct
         for field, _ in mirror._fields_:
             assert getattr(mirror, field).offset == measured[(struct, field)], (struct, field)
+
+
+def test_a_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No fallback: without the built shared object every operator raises instead of computing
+    anything another way."""
+    import torch
+
+    from uniserve_moe import ops
+
+    monkeypatch.setattr(abi, "_LIBRARY", None)
+    monkeypatch.setattr(abi, "library_path", lambda: tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="is not built"):
+        abi.library()
+    with pytest.raises(RuntimeError, match="is not built"):
+        ops.quantize_mxfp8(torch.zeros((1, 128), dtype=torch.bfloat16))
