@@ -6,8 +6,8 @@
 // One workgroup of 4 wavefronts owns one 128-row sort tile and 128 weight rows of its expert (FC1:
 // 64 up rows and the matching 64 gate rows; FC2: 128 output columns); two workgroups share a CU, so
 // each SIMD runs two waves from different workgroups: one workgroup's barrier, DMA wait or
-// epilogue is covered by the other's MFMAs (a single wave issues the scaled MFMA at only half the
-// peak rate; two interleaved waves reach it). Wave (t, w) of the 2 x 2 arrangement multiplies tile
+// epilogue is covered by the other's MFMAs, and one wave's scaling FMAs by the other's MFMAs (a
+// wave issues its VALU and MFMA instructions one after the other). Wave (t, w) of the 2 x 2 arrangement multiplies tile
 // rows 64 t .. 64 t + 63 (four 16-row token blocks) by slice rows of four 16-row weight blocks
 // (FC1: 32 up rows and the 32 gate rows of the same columns; FC2: 64 consecutive rows).
 //
