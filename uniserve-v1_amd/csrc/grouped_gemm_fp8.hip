@@ -180,9 +180,6 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    u32x4 wcur[4], wnext[4];
-    intx8 acur[kPassTiles], anext[kPassTiles];
-    float scur[2 + kPassTiles], snext[2 + kPassTiles];
     auto fetch = [&](int64_t kb, u32x4 (&w)[4], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -227,12 +224,75 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
           for (int i = 0; i < 4; ++i) acc[set][ms][i] = __builtin_fmaf(block[i], scale, acc[set][ms][i]);
         }
     };
+    if constexpr (kSplit) {
+      // The split form walks its two 16-row sets one after the other: two weight lines per scale
+      // block in flight instead of four, so the kernel holds fewer registers (144 against 179) and
+      // three waves per SIMD instead of two - a single token's 768 workgroups (235B FC1) then run
+      // in one round (FC1 26 -> 22 us). At 64 tokens the unsplit kernel keeps both sets in flight
+      // (walking them in turn there re-reads the activations: FC1 65 -> 77 us).
+      struct Block {
+        u32x4 w[2];
+        intx8 x[kPassTiles];
+        float s[1 + kPassTiles];
+      };
+      for (int set = 0; set < 2; ++set) {
+        const float *ws = set == 0 ? ws0 : ws1;
+        auto fetch1 = [&](int64_t kb, Block &d) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            d.w[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(line_row[set] + static_cast<int64_t>(i) * 8 * p.K + kb * 128));
+          d.s[0] = ws[kb];
+#pragma unroll
+          for (int ms = 0; ms < kPassTiles; ++ms) {
+            if (valid[ms]) {
+              const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
+              const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
+              d.x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                              static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+            } else {
+              d.x[ms] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+            d.s[1 + ms] = valid[ms] ? as[ms][kb] : 0.0f;
+          }
+        };
+        auto compute1 = [&](const Block &d) {
+          const u32x4 lo0 = permute16(source_lo, d.w[0]);
+          const u32x4 lo1 = permute16(source_lo, d.w[1]);
+          const u32x4 hi0 = permute16(source_hi, d.w[0]);
+          const u32x4 hi1 = permute16(source_hi, d.w[1]);
+          const u32x4 lo = upper ? lo1 : lo0;
+          const u32x4 hi = upper ? hi1 : hi0;
+          const intx8 w = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                                static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+#pragma unroll
+          for (int ms = 0; ms < kPassTiles; ++ms) {
+            const floatx4 block = mfma_16x16x128_fp8(w, d.x[ms], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
+            const float scale = d.s[0] * d.s[1 + ms];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[set][ms][i] = __builtin_fmaf(block[i], scale, acc[set][ms][i]);
+          }
+        };
+        Block cur, next;
+        if (kb_first < kb_count) fetch1(kb_first, cur);
+        for (int64_t kb = kb_first; kb < kb_count; kb += 2 * kb_step) {
+          if (kb + kb_step < kb_count) fetch1(kb + kb_step, next);
+          compute1(cur);
+          if (kb + 2 * kb_step < kb_count) fetch1(kb + 2 * kb_step, cur);
+          if (kb + kb_step < kb_count) compute1(next);
+        }
+      }
+    } else {
+    u32x4 wcur[4], wnext[4];
+    intx8 acur[kPassTiles], anext[kPassTiles];
+    float scur[2 + kPassTiles], snext[2 + kPassTiles];
     if (kb_first < kb_count) fetch(kb_first, wcur, acur, scur);
     for (int64_t kb = kb_first; kb < kb_count; kb += 2 * kb_step) {
       if (kb + kb_step < kb_count) fetch(kb + kb_step, wnext, anext, snext);
       compute(wcur, acur, scur);
       if (kb + 2 * kb_step < kb_count) fetch(kb + 2 * kb_step, wcur, acur, scur);
       if (kb + kb_step < kb_count) compute(wnext, anext, snext);
+    }
     }
     if constexpr (kSplit) {
       // Waves 1..3 hand their partial sums to wave 0, which adds them in wave order.
