@@ -54,7 +54,9 @@ def test_every_asserted_layout_is_the_mirror_s():
 
 
 def test_reference_layout_sizes():
-    # The sizes the reference's generated headers assert (SURVEY: 648 / 632 / 616 / 608 / 600).
+    # The sizes the reference's generated headers assert: crates/ops/python/src/uniserve_kernels/include/
+    # uniserve_moe_sort.h:59, uniserve_gather_gemm.h:43, uniserve_route_gemm.h:41,
+    # uniserve_moe_unpermute.h:56, uniserve_gemm.h:71.
     assert ctypes.sizeof(abi.SortCall) == 648
     assert ctypes.sizeof(abi.GatherCall) == 632
     assert ctypes.sizeof(abi.RouteCall) == 616
