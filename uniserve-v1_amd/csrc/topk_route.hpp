@@ -1,7 +1,7 @@
 // SPDX-License-Identifier: Apache-2.0
 //
-// The router's per-token routine (softmax, top-k, renormalisation, scale, map, load), shared by
-// the topk_softmax kernel and the layer's fused route-and-sort kernel.
+// The router's per-token routine (softmax, top-k, renormalisation, scale, map, load) of the
+// topk_softmax kernel.
 //
 // One token per 32-lane half of a 64-lane wavefront. The probabilities are FP32 reductions whose
 // rounding depends on their order, and the selection compares them for equality, so the routine
