@@ -53,7 +53,9 @@ def quantized_stacks(device, experts, hidden, intermediate, seed=2):
 @pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew", [
     (64, 2048, 128, 8, 768, "uniform"), (1024, 2048, 128, 8, 768, "zipf"), (5, 4096, 16, 8, 1536, "uniform"),
     # prefill kernels at their smallest shapes: two K stages, one 256-column FC2 slice, ragged tiles
-    (600, 256, 8, 2, 256, "zipf")])
+    (600, 256, 8, 2, 256, "zipf"),
+    # the split stream kernel with two 16-row blocks per pass and, on the hottest expert, two passes
+    (80, 512, 8, 2, 256, "zipf")])
 def test_fp8_products(device, tokens, hidden, experts, top, intermediate, skew):
     announce("fp8 products", tokens, hidden, experts, top, intermediate, skew)
     rng = np.random.default_rng(tokens)
