@@ -67,7 +67,9 @@ def test_stage_major_scales_are_the_row_major_bytes_regrouped(device):
     (512, 2048, 128, 8, 768, "zipf", "row"), (1024, 4096, 128, 8, 1536, "zipf", "row"),
     (64, 2048, 128, 8, 768, "uniform", "stage"), (512, 2048, 128, 8, 768, "zipf", "stage"),
     # the tiled kernel at its smallest shapes: two K stages, one weight slice, ragged tiles
-    (600, 256, 8, 2, 256, "zipf", "row")])
+    (600, 256, 8, 2, 256, "zipf", "row"),
+    # the split stream kernel over several 16-row passes of the hottest expert's tile
+    (80, 512, 8, 2, 256, "zipf", "stage")])
 def test_mx_products(device, tokens, hidden, experts, top, intermediate, skew, layout):
     announce("mx products", tokens, hidden, experts, top, intermediate, skew, layout)
     rng = np.random.default_rng(tokens + 7)
