@@ -36,6 +36,7 @@ CASES = {
     # name: tokens, hidden, experts, top, intermediate, skew
     "30b decode (stream)": (64, 2048, 128, 8, 768, "uniform"),
     "skewed decode (stream, one-row-block passes over tiles of many rows)": (128, 2048, 128, 8, 768, "zipf"),
+    "skewed decode (stream, two-row-block passes over tiles of many rows)": (256, 2048, 128, 8, 768, "zipf"),
     "reference gather shape, emptied expert": (512, 2048, 128, 8, 1536, "uniform"),
     "skewed prefill (tiled)": (1024, 2048, 128, 8, 768, "zipf"),
     "tiny": (16, 256, 8, 2, 128, "uniform"),
