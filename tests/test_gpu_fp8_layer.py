@@ -52,6 +52,8 @@ def quantized_stacks(device, experts, hidden, intermediate, seed=2):
 
 @pytest.mark.parametrize("tokens,hidden,experts,top,intermediate,skew", [
     (64, 2048, 128, 8, 768, "uniform"), (1024, 2048, 128, 8, 768, "zipf"), (5, 4096, 16, 8, 1536, "uniform"),
+    # the unsplit stream kernel with two 16-row blocks per pass, several passes on hot experts
+    (256, 2048, 128, 8, 768, "zipf"),
     # prefill kernels at their smallest shapes: two K stages, one 256-column FC2 slice, ragged tiles
     (600, 256, 8, 2, 256, "zipf"),
     # the split stream kernel with two 16-row blocks per pass and, on the hottest expert, two passes
