@@ -58,8 +58,8 @@ def quantized_stacks(device, experts, hidden, intermediate, seed=2):
     (600, 256, 8, 2, 256, "zipf"),
     # the split stream kernel with two 16-row blocks per pass and, on the hottest expert, two passes
     (80, 512, 8, 2, 256, "zipf"),
-    # widths the two-workgroup kernel does not take (FC1 on the tiled kernel, FC2 on the 8-wave one)
-    (300, 384, 16, 4, 256, "uniform")])
+    # three K stages on the two-workgroup FC1; an FC2 neither it nor the 8-wave kernel takes (tiled)
+    (300, 384, 16, 4, 384, "uniform")])
 def test_fp8_products(device, tokens, hidden, experts, top, intermediate, skew):
     announce("fp8 products", tokens, hidden, experts, top, intermediate, skew)
     rng = np.random.default_rng(tokens)

@@ -514,8 +514,11 @@ void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scal
 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream) {
-  const bool fits = gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
-                          : prefill_fits<prefill::E4m3, false>(p.K, p.out_width);
+  // The two-workgroup kernel first, then the 8-wave one (whole 256-K stage pairs), then the
+  // generic tiled kernel.
+  const bool fits = dual_fits(gated, p.K, p.out_width, p.out_codes != nullptr) ||
+                    (gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
+                           : prefill_fits<prefill::E4m3, false>(p.K, p.out_width));
   if (!stream_path && fits) {
     PrefillParams q{};
     q.act = p.act;
