@@ -40,6 +40,19 @@ enum uniserve_dtype
   UNISERVE_DTYPE_F64 = 10,
 };
 
+/// FC1's gate, the two a grouped expert product compiles (crates/ops/src/moe/grouped.rs:53-61):
+/// silu, and PyTorch's tanh approximation of GELU (crates/nn/src/functional/activation.rs:62-71).
+/// The reference compiles the gate into each FC1 module; here the FC1 entries come in one name
+/// per gate (`..._gelu_tanh` for the second), and the layer call carries it as a field.
+enum uniserve_activation
+#ifdef __cplusplus
+    : int32_t
+#endif
+{
+  UNISERVE_ACTIVATION_SILU = 0,
+  UNISERVE_ACTIVATION_GELU_TANH = 1,
+};
+
 #ifdef __cplusplus
 #define UNISERVE_EXTERN_C extern "C"
 #else

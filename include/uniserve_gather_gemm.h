@@ -1,8 +1,9 @@
 // SPDX-License-Identifier: Apache-2.0
 //
 // gather_gemm (FC1): for each live permuted row p of token t and expert e,
-//   out[p, :] = silu(W[e, I:2I] . x[t]) * (W[e, 0:I] . x[t])
-// with FP32 accumulation, the activation on the accumulators and one rounding to bf16.
+//   out[p, :] = act(W[e, I:2I] . x[t]) * (W[e, 0:I] . x[t])
+// with FP32 accumulation, the activation on the accumulators and one rounding to bf16; act is
+// silu (`uniserve_gather_gemm`) or gelu_tanh (`uniserve_gather_gemm_gelu_tanh`).
 //
 // Replaces crates/ops/kernels/gather_gemm/cute_dsl/src/entry.cpp:57-59 (`uniserve_gather_gemm`),
 // called by `GatherGemm::launch` (crates/ops/src/moe/grouped.rs:326-360). The structure is the
@@ -52,3 +53,9 @@ static_assert(offsetof(uniserve_gather_call, error) == 120, "layout");
 #endif
 
 UNISERVE_EXTERN_C int32_t uniserve_gather_gemm(const struct uniserve_gather_call *call, void *stream);
+
+/// The same call with a gelu_tanh gate: the reference compiles the gate into each FC1 module
+/// (`GatherGemmDescriptor::activation`, crates/ops/src/moe/grouped.rs:65-127, descriptors
+/// `activation = ["silu", "gelu_tanh"]` in gather_gemm/cute_dsl/package.toml), so a module built
+/// for `gelu_tanh` exports this entry under the plain name; here both live in one library.
+UNISERVE_EXTERN_C int32_t uniserve_gather_gemm_gelu_tanh(const struct uniserve_gather_call *call, void *stream);

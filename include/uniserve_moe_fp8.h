@@ -31,7 +31,8 @@ struct uniserve_quantize_fp8_call {
   char error[512];
 };
 
-/// FC1 over e4m3 operands: out[p] = silu(gate) * up with
+/// FC1 over e4m3 operands: out[p] = act(gate) * up (act: silu, or gelu_tanh for the `_gelu_tanh`
+/// entry) with
 ///   up = sum_kb (sum_{k in kb} q_x[t,k] q_w[e,n,k]) * s_x[t,kb] * s_w[e,n/128,kb]
 /// accumulated in FP32, one rounding into bf16.
 struct uniserve_gather_fp8_call {
@@ -82,4 +83,5 @@ struct uniserve_route_fp8_call {
 
 UNISERVE_EXTERN_C int32_t uniserve_quantize_fp8(const struct uniserve_quantize_fp8_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_gather_gemm_fp8(const struct uniserve_gather_fp8_call *call, void *stream);
+UNISERVE_EXTERN_C int32_t uniserve_gather_gemm_fp8_gelu_tanh(const struct uniserve_gather_fp8_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_route_gemm_fp8(const struct uniserve_route_fp8_call *call, void *stream);

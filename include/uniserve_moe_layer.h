@@ -41,6 +41,13 @@ struct uniserve_moe_layer_call {
   int64_t multiprocessors;
   int64_t weight_scale_layout; ///< MXFP4: uniserve_mx_scale_layout of both scale tables; else 0
   char error[512];
+  // What `MoE::select` and `MoE::routed` pass beyond the rows (crates/nn/src/modules/moe.rs:
+  // 650-671, 770-775), after `error` so the fields above keep their offsets; zero = absent.
+  const int32_t *map;          ///< [experts] slot of each router expert (topk writes map[e]), or null
+  int64_t *load;               ///< [experts] each live route counted by router expert, or null
+  int64_t local_offset;        ///< first slot of the window this layer's stacks hold
+  int64_t local_experts;       ///< slots the stacks hold ([local_experts, ...]); 0 = every expert
+  int64_t activation;          ///< FC1's gate: uniserve_activation (0 = silu)
 };
 
 /// Workspace bytes the call needs for these extents, or -1 for extents it does not serve.

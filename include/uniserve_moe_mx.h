@@ -49,7 +49,8 @@ struct uniserve_quantize_mxfp8_call {
   char error[512];
 };
 
-/// FC1 over MX operands: out[p] = silu(gate) * up with
+/// FC1 over MX operands: out[p] = act(gate) * up (act: silu, or gelu_tanh for the `_gelu_tanh`
+/// entry) with
 ///   up = sum_k e4m3(q_x[t,k]) 2^(s_x[t,k/32]-127) * e2m1(q_w[e,n,k]) 2^(s_w[e,n,k/32]-127)
 /// accumulated in FP32, one rounding into bf16.
 struct uniserve_gather_mx_call {
@@ -107,5 +108,6 @@ struct uniserve_mx_stage_scales_call {
 
 UNISERVE_EXTERN_C int32_t uniserve_quantize_mxfp8(const struct uniserve_quantize_mxfp8_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_gather_gemm_mx(const struct uniserve_gather_mx_call *call, void *stream);
+UNISERVE_EXTERN_C int32_t uniserve_gather_gemm_mx_gelu_tanh(const struct uniserve_gather_mx_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_route_gemm_mx(const struct uniserve_route_mx_call *call, void *stream);
 UNISERVE_EXTERN_C int32_t uniserve_mx_stage_major_scales(const struct uniserve_mx_stage_scales_call *call, void *stream);

@@ -429,23 +429,53 @@ static float dot(const float *a, const float *b, int64_t n) {
 
 static float silu(float x) { return x / (1.0f + expf(-x)); }
 
-/* The router Linear (crates/nn/src/modules/moe.rs:656-671 -> `gemm`): out = x . W^T with FP32
- * accumulation and one rounding into bf16. */
-void oracle_router_gemm(const uint16_t *x, const uint16_t *weight, int64_t m, int64_t n, int64_t k,
-                        uint16_t *out) {
+/* The gate of FC1: silu (Qwen3) or PyTorch's gelu_pytorch_tanh, 0.5 g (1 + tanh(sqrt(2/pi)
+ * (g + 0.044715 g^3))), evaluated in FP32 (crates/nn/src/functional/activation.rs:62-82; the
+ * grouped products gate with these two only, crates/ops/src/moe/grouped.rs:53-61). */
+static float gate_activation(float g, int32_t activation) {
+  if (activation == 1) return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g)));
+  return silu(g);
+}
+
+float oracle_gate_activation(float g, int32_t activation) { return gate_activation(g, activation); }
+
+/* `n` elements of kind `kind` (0 f32, 1 bf16, 2 f16) from `data` at element `offset`, widened. */
+static void widen_row(const void *data, int32_t kind, int64_t offset, int64_t n, float *out) {
+  if (kind == 0) memcpy(out, (const float *)data + offset, (size_t)n * sizeof(float));
+  else if (kind == 1) oracle_bf16_decode((const uint16_t *)data + offset, out, n);
+  else
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_from_f16(((const uint16_t *)data)[offset + i]);
+}
+
+/* The router Linear (crates/nn/src/modules/moe.rs:656-671 -> `Linear::forward`,
+ * crates/nn/src/modules/linear.rs:653-669 -> `gemm`): out = x . W^T (+ bias) with FP32
+ * accumulation, the bias added to the FP32 sum, and one rounding into the output's element type
+ * (`out_kind` 1: bf16 bits; 0: f32, no rounding). Elements of x and W are of kind `kind`. */
+void oracle_router_gemm_ex(const void *x, const void *weight, int32_t kind, const float *bias,
+                           int64_t m, int64_t n, int64_t k, int32_t out_kind, void *out) {
   float *wf = (float *)malloc((size_t)(n * k) * sizeof(float));
-  oracle_bf16_decode(weight, wf, n * k);
+  widen_row(weight, kind, 0, n * k, wf);
 #pragma omp parallel
   {
     float *xf = (float *)malloc((size_t)k * sizeof(float));
 #pragma omp for schedule(static)
     for (int64_t i = 0; i < m; ++i) {
-      oracle_bf16_decode(x + i * k, xf, k);
-      for (int64_t j = 0; j < n; ++j) out[i * n + j] = oracle_bf16_from_f32(dot(xf, wf + j * k, k));
+      widen_row(x, kind, i * k, k, xf);
+      for (int64_t j = 0; j < n; ++j) {
+        float value = dot(xf, wf + j * k, k);
+        if (bias != NULL) value += bias[j];
+        if (out_kind == 0) ((float *)out)[i * n + j] = value;
+        else ((uint16_t *)out)[i * n + j] = oracle_bf16_from_f32(value);
+      }
     }
     free(xf);
   }
   free(wf);
+}
+
+void oracle_router_gemm(const uint16_t *x, const uint16_t *weight, int64_t m, int64_t n, int64_t k,
+                        uint16_t *out) {
+  oracle_router_gemm_ex(x, weight, 1, NULL, m, n, k, 1, out);
 }
 
 /* gather_gemm's CPU formula (crates/nn/src/functional/moe.rs:554-578): per live permuted row p
@@ -454,10 +484,11 @@ void oracle_router_gemm(const uint16_t *x, const uint16_t *weight, int64_t m, in
  * out[p, :] = silu(gate) * up in FP32 (the rounding into bf16 is the caller's). The per-row
  * weight gather of the reference (`index_select(&expert)`, moe.rs:570) is evaluated per tile:
  * the same sums, grouped by expert. Rows the formula does not name are left untouched. */
-void oracle_gather_gemm(const uint16_t *hidden, const uint16_t *weights, int64_t tokens,
-                        int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
-                        const int32_t *tile_to_expert, const int32_t *tile_to_limit,
-                        const int32_t *permuted_to_expanded, int32_t num_tiles, float *out) {
+void oracle_gather_gemm_ex(const void *hidden, const void *weights, int32_t kind, int64_t tokens,
+                           int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
+                           const int32_t *tile_to_expert, const int32_t *tile_to_limit,
+                           const int32_t *permuted_to_expanded, int32_t num_tiles, int32_t activation,
+                           float *out) {
   (void)tokens;
   const int64_t width = 2 * intermediate;
 #pragma omp parallel
@@ -471,15 +502,15 @@ void oracle_gather_gemm(const uint16_t *hidden, const uint16_t *weights, int64_t
       const int64_t first = (int64_t)t * tile;
       const int64_t rows = tile_to_limit[t] - first;
       for (int64_t r = 0; r < rows; ++r)
-        oracle_bf16_decode(hidden + (permuted_to_expanded[first + r] / top) * hidden_size,
-                           x + r * hidden_size, hidden_size);
+        widen_row(hidden, kind, (permuted_to_expanded[first + r] / top) * hidden_size, hidden_size,
+                  x + r * hidden_size);
       for (int64_t n = 0; n < width; ++n) {
-        oracle_bf16_decode(weights + (e * width + n) * hidden_size, w, hidden_size);
+        widen_row(weights, kind, (e * width + n) * hidden_size, hidden_size, w);
         for (int64_t r = 0; r < rows; ++r) {
           const float value = dot(x + r * hidden_size, w, hidden_size);
           if (n < intermediate) up[r * intermediate + n] = value;
           else out[(first + r) * intermediate + (n - intermediate)] =
-                   silu(value) * up[r * intermediate + (n - intermediate)];
+                   gate_activation(value, activation) * up[r * intermediate + (n - intermediate)];
         }
       }
     }
@@ -489,11 +520,19 @@ void oracle_gather_gemm(const uint16_t *hidden, const uint16_t *weights, int64_t
   }
 }
 
+void oracle_gather_gemm(const uint16_t *hidden, const uint16_t *weights, int64_t tokens,
+                        int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
+                        const int32_t *tile_to_expert, const int32_t *tile_to_limit,
+                        const int32_t *permuted_to_expanded, int32_t num_tiles, float *out) {
+  oracle_gather_gemm_ex(hidden, weights, 1, tokens, hidden_size, intermediate, top, tile, tile_to_expert,
+                        tile_to_limit, permuted_to_expanded, num_tiles, 0, out);
+}
+
 /* route_gemm's CPU formula (crates/nn/src/functional/moe.rs:706-723): out[p, :] =
  * W[e] . rows[p] in FP32 for the live rows of every live tile. */
-void oracle_route_gemm(const uint16_t *rows, const uint16_t *weights, int64_t hidden_size,
-                       int64_t intermediate, int64_t tile, const int32_t *tile_to_expert,
-                       const int32_t *tile_to_limit, int32_t num_tiles, float *out) {
+void oracle_route_gemm_ex(const void *rows, const void *weights, int32_t kind, int64_t hidden_size,
+                          int64_t intermediate, int64_t tile, const int32_t *tile_to_expert,
+                          const int32_t *tile_to_limit, int32_t num_tiles, float *out) {
 #pragma omp parallel
   {
     float *w = (float *)malloc((size_t)intermediate * sizeof(float));
@@ -503,9 +542,9 @@ void oracle_route_gemm(const uint16_t *rows, const uint16_t *weights, int64_t hi
       const int64_t e = tile_to_expert[t];
       const int64_t first = (int64_t)t * tile;
       const int64_t count = tile_to_limit[t] - first;
-      oracle_bf16_decode(rows + first * intermediate, x, count * intermediate);
+      widen_row(rows, kind, first * intermediate, count * intermediate, x);
       for (int64_t n = 0; n < hidden_size; ++n) {
-        oracle_bf16_decode(weights + (e * hidden_size + n) * intermediate, w, intermediate);
+        widen_row(weights, kind, (e * hidden_size + n) * intermediate, intermediate, w);
         for (int64_t r = 0; r < count; ++r)
           out[(first + r) * hidden_size + n] = dot(x + r * intermediate, w, intermediate);
       }
@@ -515,26 +554,44 @@ void oracle_route_gemm(const uint16_t *rows, const uint16_t *weights, int64_t hi
   }
 }
 
+void oracle_route_gemm(const uint16_t *rows, const uint16_t *weights, int64_t hidden_size,
+                       int64_t intermediate, int64_t tile, const int32_t *tile_to_expert,
+                       const int32_t *tile_to_limit, int32_t num_tiles, float *out) {
+  oracle_route_gemm_ex(rows, weights, 1, hidden_size, intermediate, tile, tile_to_expert, tile_to_limit,
+                       num_tiles, out);
+}
+
 /* moe_unpermute (crates/ops/src/moe/combine.rs:1-17, CPU formula crates/nn/src/functional/moe.rs:
  * 1258-1291): out[t] = sum over k in route order of scales[t,k] * routes[row] in FP32, a route
  * whose map entry is negative (or past the routes' rows) contributing nothing; row =
  * expanded_to_permuted[t,k] in the permuted layout, t * top + k in the expanded one. */
+void oracle_moe_unpermute_ex(const void *routes, int32_t kind, const int32_t *expanded_to_permuted,
+                             const float *scales, int64_t tokens, int64_t top, int64_t hidden,
+                             int64_t routes_rows, int32_t layout, float *out) {
+#pragma omp parallel
+  {
+    float *row_values = (float *)malloc((size_t)hidden * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < tokens; ++t) {
+      float *sum = out + t * hidden;
+      for (int64_t h = 0; h < hidden; ++h) sum[h] = 0.0f;
+      for (int64_t k = 0; k < top; ++k) {
+        const int64_t entry = expanded_to_permuted[t * top + k];
+        if (entry < 0 || entry >= routes_rows) continue;
+        const int64_t row = layout == 1 ? t * top + k : entry;
+        const float w = scales[t * top + k];
+        widen_row(routes, kind, row * hidden, hidden, row_values);
+        for (int64_t h = 0; h < hidden; ++h) sum[h] += w * row_values[h];
+      }
+    }
+    free(row_values);
+  }
+}
+
 void oracle_moe_unpermute(const uint16_t *routes, const int32_t *expanded_to_permuted,
                           const float *scales, int64_t tokens, int64_t top, int64_t hidden,
                           int64_t routes_rows, int32_t layout, float *out) {
-#pragma omp parallel for schedule(static)
-  for (int64_t t = 0; t < tokens; ++t) {
-    float *sum = out + t * hidden;
-    for (int64_t h = 0; h < hidden; ++h) sum[h] = 0.0f;
-    for (int64_t k = 0; k < top; ++k) {
-      const int64_t entry = expanded_to_permuted[t * top + k];
-      if (entry < 0 || entry >= routes_rows) continue;
-      const int64_t row = layout == 1 ? t * top + k : entry;
-      const float w = scales[t * top + k];
-      for (int64_t h = 0; h < hidden; ++h)
-        sum[h] += w * oracle_f32_from_bf16(routes[row * hidden + h]);
-    }
-  }
+  oracle_moe_unpermute_ex(routes, 1, expanded_to_permuted, scales, tokens, top, hidden, routes_rows, layout, out);
 }
 
 /* sigmoid_gated_add (crates/ops/src/residual.rs:808-811; CPU form crates/nn/src/functional/moe.rs:1589-1600):
@@ -633,7 +690,8 @@ void oracle_gather_gemm_fp8(const uint8_t *hidden, const float *hidden_scales,
                             const uint8_t *weights, const float *weight_scales, int64_t tokens,
                             int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
                             const int32_t *tile_to_expert, const int32_t *tile_to_limit,
-                            const int32_t *permuted_to_expanded, int32_t num_tiles, float *out) {
+                            const int32_t *permuted_to_expanded, int32_t num_tiles, int32_t activation,
+                            float *out) {
   (void)tokens;
   const int64_t width = 2 * intermediate, kb = hidden_size / 128, nb = width / 128;
 #pragma omp parallel
@@ -653,7 +711,7 @@ void oracle_gather_gemm_fp8(const uint8_t *hidden, const float *hidden_scales,
             v[half] = dot_fp8(hidden + token * hidden_size, hidden_scales + token * kb,
                               weights + (e * width + row) * hidden_size, sb, hidden_size, 128);
           }
-          out[p * intermediate + n] = silu(v[1]) * v[0];
+          out[p * intermediate + n] = gate_activation(v[1], activation) * v[0];
         }
       }
     }
@@ -799,7 +857,7 @@ void oracle_gather_gemm_mx(const uint8_t *hidden, const uint8_t *hidden_scales, 
                            const uint8_t *weight_scales, int64_t tokens, int64_t hidden_size,
                            int64_t intermediate, int64_t top, int64_t tile, const int32_t *tile_to_expert,
                            const int32_t *tile_to_limit, const int32_t *permuted_to_expanded,
-                           int32_t num_tiles, float *out) {
+                           int32_t num_tiles, int32_t activation, float *out) {
   (void)tokens;
   const int64_t width = 2 * intermediate, kb = hidden_size / 32;
 #pragma omp parallel for schedule(dynamic, 1)
@@ -814,7 +872,7 @@ void oracle_gather_gemm_mx(const uint8_t *hidden, const uint8_t *hidden_scales, 
           v[half] = dot_mx(hidden + token * hidden_size, hidden_scales + token * kb, weights + row * (hidden_size / 2),
                            weight_scales + row * kb, hidden_size);
         }
-        out[p * intermediate + n] = silu(v[1]) * v[0];
+        out[p * intermediate + n] = gate_activation(v[1], activation) * v[0];
       }
     }
   }
@@ -847,20 +905,23 @@ int32_t oracle_threads(void) {
 #endif
 }
 
-/* MoE::routed (crates/nn/src/modules/moe.rs:770-795) on the CPU: router gemm (bf16 scores) ->
- * topk (renormalised) -> sort -> FC1 (gated rows rounded to bf16) -> FC2 (products rounded to
- * bf16) -> combine (FP32, one rounding into bf16), the reference's rounding points. For e4m3
- * weights (6) the activations of each product are quantised per row per 128 channels first; for
- * MX weights (7: E2M1 codes, E8M0 scale bytes) per row per 32 channels to MXFP8. */
-int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const void *up_gate,
-                         const float *up_gate_scales, const void *down, const float *down_scales,
-                         int64_t tokens, int64_t hidden_size, int64_t experts, int64_t top,
-                         int64_t intermediate, int32_t renormalize, int32_t weight_dtype,
-                         uint16_t *out, int32_t *ids_out, float *weights_out) {
-  const int64_t tile = 128;
-  const int64_t tiles = oracle_max_tiles(tokens, top, experts, tile);
+/* MoE::routed (crates/nn/src/modules/moe.rs:770-795) on the CPU, `MoE::select` (:656-671)
+ * included: router gemm (+ bias, scores in the hidden rows' element type) -> topk (the slot map,
+ * the live rows' load) -> sort (over the local window, live rows only) -> FC1 -> FC2 -> combine.
+ * Rounding points are the reference's: for bf16 rows the scores, the gated rows and the products
+ * round into bf16, the combine sums in FP32 and rounds once; for f32 rows (weight_dtype 5,
+ * the CPU reference path of crates/nn/src/functional/moe.rs:554-578, 706-723, 1258-1291) nothing
+ * rounds. For e4m3 weights (6) the activations of each product are quantised per row per 128
+ * channels first; for MX weights (7: E2M1 codes, E8M0 scale bytes) per row per 32 channels to
+ * MXFP8. The stacks hold the window's experts only: [local_experts, ...]. */
+int32_t oracle_moe_layer_ex(const oracle_layer_call *c) {
+  const int64_t tile = 128, tokens = c->tokens, hidden_size = c->hidden_size, experts = c->experts;
+  const int64_t top = c->top, intermediate = c->intermediate;
+  const int64_t local_experts = c->local_experts > 0 ? c->local_experts : experts;
+  const int32_t f32 = c->weight_dtype == 5, kind = f32 ? 0 : 1;
+  const int64_t tiles = oracle_max_tiles(tokens, top, local_experts, tile);
   const int64_t rows = tiles * tile;
-  uint16_t *scores = (uint16_t *)malloc((size_t)(tokens * experts) * 2);
+  void *scores = malloc((size_t)(tokens * experts) * (f32 ? 4 : 2));
   int32_t *ids = (int32_t *)malloc((size_t)(tokens * top) * 4);
   float *weights = (float *)malloc((size_t)(tokens * top) * 4);
   int32_t *t2e = (int32_t *)calloc((size_t)tiles + 1, 4), *t2l = (int32_t *)calloc((size_t)tiles + 1, 4);
@@ -872,52 +933,87 @@ int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const v
   float *products = (float *)calloc((size_t)(rows * hidden_size), 4);
   uint16_t *products_bf16 = (uint16_t *)malloc((size_t)(rows * hidden_size) * 2);
   float *combined = (float *)malloc((size_t)(tokens * hidden_size) * 4);
+  const uint16_t *hidden = (const uint16_t *)c->hidden;
 
-  oracle_router_gemm(hidden, router, tokens, experts, hidden_size, scores);
-  oracle_topk_softmax(scores, 1, experts, (int32_t)tokens, (int32_t)experts, (int32_t)top,
-                      renormalize, NULL, -1, ids, weights, NULL, NULL, NULL);
-  oracle_moe_sort(ids, tokens, top, experts, 0, tile, NULL, t2e, t2l, e2p, p2e, p2t, &padded,
-                  &live_tiles);
-  if (weight_dtype == 6) {
+  oracle_router_gemm_ex(c->hidden, c->router, kind, c->router_bias, tokens, experts, hidden_size, kind, scores);
+  oracle_topk_softmax(scores, kind, experts, (int32_t)tokens, (int32_t)experts, (int32_t)top, c->renormalize,
+                      NULL, -1, ids, weights, c->map, c->live_tokens, c->load);
+  oracle_moe_sort(ids, tokens, top, local_experts, c->local_offset, tile, c->live_tokens, t2e, t2l, e2p, p2e, p2t,
+                  &padded, &live_tiles);
+  if (c->weight_dtype == 6) {
     uint8_t *xq = (uint8_t *)malloc((size_t)(tokens * hidden_size));
     float *xs = (float *)malloc((size_t)(tokens * hidden_size / 128) * 4);
     oracle_quantize_rows_fp8(hidden, tokens, hidden_size, 128, xq, xs);
-    oracle_gather_gemm_fp8(xq, xs, (const uint8_t *)up_gate, up_gate_scales, tokens, hidden_size,
-                           intermediate, top, tile, t2e, t2l, p2e, live_tiles, gated);
+    oracle_gather_gemm_fp8(xq, xs, (const uint8_t *)c->up_gate, (const float *)c->up_gate_scales, tokens,
+                           hidden_size, intermediate, top, tile, t2e, t2l, p2e, live_tiles, c->activation, gated);
     oracle_bf16_encode(gated, gated_bf16, (int64_t)padded * intermediate);
     uint8_t *gq = (uint8_t *)malloc((size_t)(rows * intermediate));
     float *gs = (float *)malloc((size_t)(rows * intermediate / 128) * 4);
     oracle_quantize_rows_fp8(gated_bf16, padded, intermediate, 128, gq, gs);
-    oracle_route_gemm_fp8(gq, gs, (const uint8_t *)down, down_scales, hidden_size, intermediate,
-                          tile, t2e, t2l, live_tiles, products);
+    oracle_route_gemm_fp8(gq, gs, (const uint8_t *)c->down, (const float *)c->down_scales, hidden_size,
+                          intermediate, tile, t2e, t2l, live_tiles, products);
     free(xq); free(xs); free(gq); free(gs);
-  } else if (weight_dtype == 7) {
-    /* MX: E2M1 weights with E8M0 scales (the scale pointers are bytes), MXFP8 activations. */
+  } else if (c->weight_dtype == 7) {
     uint8_t *xq = (uint8_t *)malloc((size_t)(tokens * hidden_size));
     uint8_t *xs = (uint8_t *)malloc((size_t)(tokens * hidden_size / 32));
     oracle_quantize_rows_mxfp8(hidden, tokens, hidden_size, xq, xs);
-    oracle_gather_gemm_mx(xq, xs, (const uint8_t *)up_gate, (const uint8_t *)up_gate_scales, tokens, hidden_size,
-                          intermediate, top, tile, t2e, t2l, p2e, live_tiles, gated);
+    oracle_gather_gemm_mx(xq, xs, (const uint8_t *)c->up_gate, (const uint8_t *)c->up_gate_scales, tokens,
+                          hidden_size, intermediate, top, tile, t2e, t2l, p2e, live_tiles, c->activation, gated);
     oracle_bf16_encode(gated, gated_bf16, (int64_t)padded * intermediate);
     uint8_t *gq = (uint8_t *)malloc((size_t)(rows * intermediate));
     uint8_t *gs = (uint8_t *)malloc((size_t)(rows * intermediate / 32));
     oracle_quantize_rows_mxfp8(gated_bf16, padded, intermediate, gq, gs);
-    oracle_route_gemm_mx(gq, gs, (const uint8_t *)down, (const uint8_t *)down_scales, hidden_size, intermediate,
-                         tile, t2e, t2l, live_tiles, products);
+    oracle_route_gemm_mx(gq, gs, (const uint8_t *)c->down, (const uint8_t *)c->down_scales, hidden_size,
+                         intermediate, tile, t2e, t2l, live_tiles, products);
     free(xq); free(xs); free(gq); free(gs);
+  } else if (f32) {
+    oracle_gather_gemm_ex(c->hidden, c->up_gate, 0, tokens, hidden_size, intermediate, top, tile, t2e, t2l, p2e,
+                          live_tiles, c->activation, gated);
+    oracle_route_gemm_ex(gated, c->down, 0, hidden_size, intermediate, tile, t2e, t2l, live_tiles, products);
   } else {
-    oracle_gather_gemm(hidden, (const uint16_t *)up_gate, tokens, hidden_size, intermediate, top,
-                       tile, t2e, t2l, p2e, live_tiles, gated);
+    oracle_gather_gemm_ex(c->hidden, c->up_gate, 1, tokens, hidden_size, intermediate, top, tile, t2e, t2l, p2e,
+                          live_tiles, c->activation, gated);
     oracle_bf16_encode(gated, gated_bf16, (int64_t)padded * intermediate);
-    oracle_route_gemm(gated_bf16, (const uint16_t *)down, hidden_size, intermediate, tile, t2e,
-                      t2l, live_tiles, products);
+    oracle_route_gemm_ex(gated_bf16, c->down, 1, hidden_size, intermediate, tile, t2e, t2l, live_tiles, products);
   }
-  oracle_bf16_encode(products, products_bf16, (int64_t)padded * hidden_size);
-  oracle_moe_unpermute(products_bf16, e2p, weights, tokens, top, hidden_size, rows, 0, combined);
-  oracle_bf16_encode(combined, out, tokens * hidden_size);
-  if (ids_out) memcpy(ids_out, ids, (size_t)(tokens * top) * 4);
-  if (weights_out) memcpy(weights_out, weights, (size_t)(tokens * top) * 4);
+  if (f32) {
+    oracle_moe_unpermute_ex(products, 0, e2p, weights, tokens, top, hidden_size, rows, 0, (float *)c->out);
+  } else {
+    oracle_bf16_encode(products, products_bf16, (int64_t)padded * hidden_size);
+    oracle_moe_unpermute_ex(products_bf16, 1, e2p, weights, tokens, top, hidden_size, rows, 0, combined);
+    oracle_bf16_encode(combined, (uint16_t *)c->out, tokens * hidden_size);
+  }
+  if (c->ids) memcpy(c->ids, ids, (size_t)(tokens * top) * 4);
+  if (c->weights) memcpy(c->weights, weights, (size_t)(tokens * top) * 4);
+  if (c->scores) memcpy(c->scores, scores, (size_t)(tokens * experts) * (f32 ? 4 : 2));
   free(scores); free(ids); free(weights); free(t2e); free(t2l); free(e2p); free(p2e); free(p2t);
   free(gated); free(gated_bf16); free(products); free(products_bf16); free(combined);
   return oracle_threads();
+}
+
+/* The plain call: bf16 rows, every expert, no bias, map, load or live count, silu. */
+int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const void *up_gate,
+                         const float *up_gate_scales, const void *down, const float *down_scales,
+                         int64_t tokens, int64_t hidden_size, int64_t experts, int64_t top,
+                         int64_t intermediate, int32_t renormalize, int32_t weight_dtype,
+                         uint16_t *out, int32_t *ids_out, float *weights_out) {
+  oracle_layer_call c;
+  memset(&c, 0, sizeof(c));
+  c.hidden = hidden;
+  c.router = router;
+  c.up_gate = up_gate;
+  c.up_gate_scales = up_gate_scales;
+  c.down = down;
+  c.down_scales = down_scales;
+  c.tokens = tokens;
+  c.hidden_size = hidden_size;
+  c.experts = experts;
+  c.top = top;
+  c.intermediate = intermediate;
+  c.renormalize = renormalize;
+  c.weight_dtype = weight_dtype;
+  c.out = out;
+  c.ids = ids_out;
+  c.weights = weights_out;
+  return oracle_moe_layer_ex(&c);
 }

@@ -51,6 +51,22 @@ void oracle_moe_sort(const int32_t *ids, int64_t tokens, int64_t top, int64_t lo
 
 void oracle_router_gemm(const uint16_t *x, const uint16_t *weight, int64_t m, int64_t n, int64_t k,
                         uint16_t *out);
+/* kind / out_kind: 0 f32, 1 bf16 bits; bias [n] f32 or NULL, added to the FP32 sum before rounding. */
+void oracle_router_gemm_ex(const void *x, const void *weight, int32_t kind, const float *bias,
+                           int64_t m, int64_t n, int64_t k, int32_t out_kind, void *out);
+/* FC1's gate: activation 0 silu, 1 gelu_tanh. */
+float oracle_gate_activation(float g, int32_t activation);
+void oracle_gather_gemm_ex(const void *hidden, const void *weights, int32_t kind, int64_t tokens,
+                           int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
+                           const int32_t *tile_to_expert, const int32_t *tile_to_limit,
+                           const int32_t *permuted_to_expanded, int32_t num_tiles, int32_t activation,
+                           float *out);
+void oracle_route_gemm_ex(const void *rows, const void *weights, int32_t kind, int64_t hidden_size,
+                          int64_t intermediate, int64_t tile, const int32_t *tile_to_expert,
+                          const int32_t *tile_to_limit, int32_t num_tiles, float *out);
+void oracle_moe_unpermute_ex(const void *routes, int32_t kind, const int32_t *expanded_to_permuted,
+                             const float *scales, int64_t tokens, int64_t top, int64_t hidden,
+                             int64_t routes_rows, int32_t layout, float *out);
 
 void oracle_gather_gemm(const uint16_t *hidden, const uint16_t *weights, int64_t tokens,
                         int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
@@ -79,7 +95,8 @@ void oracle_gather_gemm_fp8(const uint8_t *hidden, const float *hidden_scales,
                             const uint8_t *weights, const float *weight_scales, int64_t tokens,
                             int64_t hidden_size, int64_t intermediate, int64_t top, int64_t tile,
                             const int32_t *tile_to_expert, const int32_t *tile_to_limit,
-                            const int32_t *permuted_to_expanded, int32_t num_tiles, float *out);
+                            const int32_t *permuted_to_expanded, int32_t num_tiles, int32_t activation,
+                            float *out);
 void oracle_route_gemm_fp8(const uint8_t *rows, const float *row_scales, const uint8_t *weights,
                            const float *weight_scales, int64_t hidden_size, int64_t intermediate,
                            int64_t tile, const int32_t *tile_to_expert,
@@ -97,7 +114,7 @@ void oracle_gather_gemm_mx(const uint8_t *hidden, const uint8_t *hidden_scales, 
                            const uint8_t *weight_scales, int64_t tokens, int64_t hidden_size,
                            int64_t intermediate, int64_t top, int64_t tile, const int32_t *tile_to_expert,
                            const int32_t *tile_to_limit, const int32_t *permuted_to_expanded,
-                           int32_t num_tiles, float *out);
+                           int32_t num_tiles, int32_t activation, float *out);
 void oracle_route_gemm_mx(const uint8_t *rows, const uint8_t *row_scales, const uint8_t *weights,
                           const uint8_t *weight_scales, int64_t hidden_size, int64_t intermediate, int64_t tile,
                           const int32_t *tile_to_expert, const int32_t *tile_to_limit, int32_t num_tiles,
@@ -112,6 +129,41 @@ int32_t oracle_moe_layer(const uint16_t *hidden, const uint16_t *router, const v
                          int64_t tokens, int64_t hidden_size, int64_t experts, int64_t top,
                          int64_t intermediate, int32_t renormalize, int32_t weight_dtype,
                          uint16_t *out, int32_t *ids_out, float *weights_out);
+
+/* The composed layer with everything MoE::routed passes (crates/nn/src/modules/moe.rs:650-795).
+ * weight_dtype 5 = f32 (hidden, router, up_gate, down, out all f32: the CPU reference path),
+ * 4 = bf16, 6 = e4m3, 7 = MX as above (hidden, router and out bf16 bits). The stacks hold the
+ * window's experts [local_experts, ...]; local_experts 0 means every expert. Optional (NULL):
+ * router_bias [experts] f32, map [experts], load [experts] (incremented), live_tokens [1],
+ * ids / weights / scores outputs (scores in the hidden rows' element type). */
+typedef struct oracle_layer_call {
+  const void *hidden;
+  const void *router;
+  const float *router_bias;
+  const void *up_gate;
+  const void *up_gate_scales;
+  const void *down;
+  const void *down_scales;
+  const int32_t *map;
+  int64_t *load;
+  const int32_t *live_tokens;
+  int64_t tokens;
+  int64_t hidden_size;
+  int64_t experts;
+  int64_t top;
+  int64_t intermediate;
+  int64_t local_offset;
+  int64_t local_experts;
+  int32_t renormalize;
+  int32_t weight_dtype;
+  int32_t activation;
+  int32_t reserved;
+  void *out;
+  int32_t *ids;
+  float *weights;
+  void *scores;
+} oracle_layer_call;
+int32_t oracle_moe_layer_ex(const oracle_layer_call *call);
 int32_t oracle_threads(void);
 
 #ifdef __cplusplus

@@ -42,22 +42,39 @@ _sig("oracle_max_tiles", [_I64, _I64, _I64, _I64], _I64)
 _sig("oracle_topk_softmax", [_P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _P, _P])
 _sig("oracle_moe_sort", [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P])
 _sig("oracle_router_gemm", [_P, _P, _I64, _I64, _I64, _P])
+_sig("oracle_router_gemm_ex", [_P, _P, _I32, _P, _I64, _I64, _I64, _I32, _P])
+_sig("oracle_gate_activation", [ctypes.c_float, _I32], ctypes.c_float)
+_sig("oracle_gather_gemm_ex", [_P, _P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _I32, _P])
 _sig("oracle_gather_gemm", [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P])
 _sig("oracle_route_gemm", [_P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
 _sig("oracle_moe_unpermute", [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P])
 _sig("oracle_quantize_rows_fp8", [_P, _I64, _I64, _I64, _P, _P])
 _sig("oracle_quantize_blocks_fp8", [_P, _I64, _I64, _I64, _I64, _P, _P])
-_sig("oracle_gather_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P])
+_sig("oracle_gather_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _I32, _P])
 _sig("oracle_route_gemm_fp8", [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
 _sig("oracle_moe_layer", [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _P, _P, _P], _I32)
 _sig("oracle_threads", [], _I32)
+
+
+class LayerCall(ctypes.Structure):
+    """``oracle_layer_call`` (oracle/moe_oracle.h)."""
+
+    _fields_ = [(name, _P) for name in ("hidden", "router", "router_bias", "up_gate", "up_gate_scales", "down",
+                                         "down_scales", "map", "load", "live_tokens")] + \
+        [(name, _I64) for name in ("tokens", "hidden_size", "experts", "top", "intermediate", "local_offset",
+                                   "local_experts")] + \
+        [(name, _I32) for name in ("renormalize", "weight_dtype", "activation", "reserved")] + \
+        [(name, _P) for name in ("out", "ids", "weights", "scores")]
+
+
+_sig("oracle_moe_layer_ex", [ctypes.POINTER(LayerCall)], _I32)
 _sig("oracle_sigmoid_gated_add", [_P, _P, _P, _I64, _I64, _I32])
 _sig("oracle_f32_from_e2m1", [ctypes.c_uint8], ctypes.c_float)
 _sig("oracle_e2m1_from_f32", [ctypes.c_float], ctypes.c_uint8)
 _sig("oracle_mx_scale", [ctypes.c_float, ctypes.c_float], ctypes.c_uint8)
 _sig("oracle_quantize_rows_mxfp8", [_P, _I64, _I64, _P, _P])
 _sig("oracle_quantize_blocks_mxfp4", [_P, _I64, _I64, _I64, _P, _P])
-_sig("oracle_gather_gemm_mx", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P])
+_sig("oracle_gather_gemm_mx", [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _I32, _P])
 _sig("oracle_route_gemm_mx", [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _I32, _P])
 
 KINDS = {np.dtype(np.float32): 0, "bf16": 1, np.dtype(np.float16): 2}
@@ -171,14 +188,14 @@ def e2m1_unpack(packed):
     return out
 
 
-def gather_gemm_mx(hq, hs, wq, ws, top, sort, rows, fill=np.nan):
+def gather_gemm_mx(hq, hs, wq, ws, top, sort, rows, fill=np.nan, activation=0):
     tokens, hidden = hq.shape
     experts, width, _ = wq.shape
     out = np.full((rows, width // 2), fill, dtype=np.float32)
     LIB.oracle_gather_gemm_mx(_p(_c(hq, np.uint8)), _p(_c(hs, np.uint8)), _p(_c(wq, np.uint8)), _p(_c(ws, np.uint8)),
                               tokens, hidden, width // 2, top, 128, _p(sort["tile_to_expert"]),
                               _p(sort["tile_to_limit"]), _p(sort["permuted_to_expanded"]),
-                              int(sort["num_non_exiting_tiles"][0]), _p(out))
+                              int(sort["num_non_exiting_tiles"][0]), activation, _p(out))
     return out
 
 
@@ -237,23 +254,46 @@ def moe_sort(ids, local_experts, local_offset=0, live=None, tile=128, fill=-7):
     return out
 
 
-def router_gemm(x_bits, w_bits):
+def router_gemm(x_bits, w_bits, bias=None):
+    """bf16 scores of bf16 rows, the optional f32 bias added to the FP32 sum before rounding."""
     x_bits, w_bits = _c(x_bits, np.uint16), _c(w_bits, np.uint16)
     m, k = x_bits.shape
     n = w_bits.shape[0]
     out = np.empty((m, n), dtype=np.uint16)
-    LIB.oracle_router_gemm(_p(x_bits), _p(w_bits), m, n, k, _p(out))
+    if bias is None:
+        LIB.oracle_router_gemm(_p(x_bits), _p(w_bits), m, n, k, _p(out))
+    else:
+        bias = _c(bias, np.float32)
+        LIB.oracle_router_gemm_ex(_p(x_bits), _p(w_bits), 1, _p(bias), m, n, k, 1, _p(out))
     return out
 
 
-def gather_gemm(hidden_bits, weight_bits, top, sort, rows, fill=np.nan):
-    hidden_bits, weight_bits = _c(hidden_bits, np.uint16), _c(weight_bits, np.uint16)
+def router_gemm_f32(x, w, bias=None):
+    """f32 scores of f32 rows (the CPU reference path): no rounding."""
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), dtype=np.float32)
+    LIB.oracle_router_gemm_ex(_p(x), _p(w), 0, _p(None if bias is None else _c(bias, np.float32)), m, n, k, 0, _p(out))
+    return out
+
+
+def gate_activation(g, activation):
+    return LIB.oracle_gate_activation(g, activation)
+
+
+def gather_gemm(hidden_bits, weight_bits, top, sort, rows, fill=np.nan, activation=0):
+    """FC1 of bf16 rows (activation 0 silu, 1 gelu_tanh); f32 rows when the inputs are float32."""
+    kind = 0 if np.asarray(hidden_bits).dtype == np.float32 else 1
+    dtype = np.float32 if kind == 0 else np.uint16
+    hidden_bits, weight_bits = _c(hidden_bits, dtype), _c(weight_bits, dtype)
     tokens, hidden = hidden_bits.shape
     intermediate = weight_bits.shape[1] // 2
     out = np.full((rows, intermediate), fill, dtype=np.float32)
-    LIB.oracle_gather_gemm(_p(hidden_bits), _p(weight_bits), tokens, hidden, intermediate, top, 128,
-                           _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
-                           _p(sort["permuted_to_expanded"]), int(sort["num_non_exiting_tiles"][0]), _p(out))
+    LIB.oracle_gather_gemm_ex(_p(hidden_bits), _p(weight_bits), kind, tokens, hidden, intermediate, top, 128,
+                              _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
+                              _p(sort["permuted_to_expanded"]), int(sort["num_non_exiting_tiles"][0]), activation,
+                              _p(out))
     return out
 
 
@@ -297,14 +337,15 @@ def quantize_blocks_fp8(bits, block=128):
     return out, scales
 
 
-def gather_gemm_fp8(hq, hs, wq, ws, top, sort, rows, fill=np.nan):
+def gather_gemm_fp8(hq, hs, wq, ws, top, sort, rows, fill=np.nan, activation=0):
     tokens, hidden = hq.shape
     intermediate = wq.shape[1] // 2
     out = np.full((rows, intermediate), fill, dtype=np.float32)
     LIB.oracle_gather_gemm_fp8(_p(_c(hq, np.uint8)), _p(_c(hs, np.float32)), _p(_c(wq, np.uint8)),
                                _p(_c(ws, np.float32)), tokens, hidden, intermediate, top, 128,
                                _p(sort["tile_to_expert"]), _p(sort["tile_to_limit"]),
-                               _p(sort["permuted_to_expanded"]), int(sort["num_non_exiting_tiles"][0]), _p(out))
+                               _p(sort["permuted_to_expanded"]), int(sort["num_non_exiting_tiles"][0]), activation,
+                               _p(out))
     return out
 
 
@@ -320,20 +361,54 @@ def route_gemm_fp8(gq, gs, wq, ws, sort, fill=np.nan):
 
 
 def moe_layer(hidden_bits, router_bits, up_gate, down, top, renormalize=True, up_gate_scales=None,
-              down_scales=None):
-    """The composed layer on the CPU; answers (out bf16 bits, ids, weights, threads)."""
-    hidden_bits, router_bits = _c(hidden_bits, np.uint16), _c(router_bits, np.uint16)
+              down_scales=None, router_bias=None, mapping=None, load=None, live=None, window=None, activation=0,
+              scores=False):
+    """The composed layer on the CPU; answers (out, ids, weights, threads) and, with ``scores``, the
+    router scores last. bf16 bits in and out, or float32 everything (the CPU reference path) when
+    ``hidden_bits`` is float32. ``window`` = (local_offset, local_experts): the stacks hold those
+    experts only. ``load`` (int64 [experts]) is incremented in place."""
+    f32 = np.asarray(hidden_bits).dtype == np.float32
+    elem = np.float32 if f32 else np.uint16
+    hidden_bits, router_bits = _c(hidden_bits, elem), _c(router_bits, elem)
     tokens, hidden = hidden_bits.shape
     experts = router_bits.shape[0]
     intermediate = up_gate.shape[1] // 2
     # MX stacks: E2M1 pairs with E8M0 byte scales; e4m3: bytes with f32 scales.
     mx = up_gate_scales is not None and np.asarray(up_gate_scales).dtype == np.uint8
     fp8 = up_gate.dtype == np.uint8 and not mx
-    out = np.empty((tokens, hidden), dtype=np.uint16)
+    out = np.empty((tokens, hidden), dtype=elem)
     ids = np.empty((tokens, top), dtype=np.int32)
     weights = np.empty((tokens, top), dtype=np.float32)
-    threads = LIB.oracle_moe_layer(_p(hidden_bits), _p(router_bits), _p(np.ascontiguousarray(up_gate)),
-                                   _p(up_gate_scales), _p(np.ascontiguousarray(down)), _p(down_scales),
-                                   tokens, hidden, experts, top, intermediate, 1 if renormalize else 0,
-                                   7 if mx else 6 if fp8 else 4, _p(out), _p(ids), _p(weights))
+    score_out = np.empty((tokens, experts), dtype=elem)
+    keep = []
+
+    def ptr(array, dtype):
+        if array is None:
+            return None
+        array = _c(array, dtype)
+        keep.append(array)
+        return array.ctypes.data
+
+    if load is not None:
+        assert load.dtype == np.int64 and load.flags.c_contiguous
+    call = LayerCall()
+    call.hidden, call.router = hidden_bits.ctypes.data, router_bits.ctypes.data
+    call.router_bias = ptr(router_bias, np.float32)
+    call.up_gate = ptr(up_gate, up_gate.dtype)
+    call.up_gate_scales = ptr(up_gate_scales, None if up_gate_scales is None else np.asarray(up_gate_scales).dtype)
+    call.down = ptr(down, down.dtype)
+    call.down_scales = ptr(down_scales, None if down_scales is None else np.asarray(down_scales).dtype)
+    call.map = ptr(mapping, np.int32)
+    call.load = None if load is None else load.ctypes.data
+    call.live_tokens = ptr(None if live is None else np.array([live], np.int32), np.int32)
+    call.tokens, call.hidden_size, call.experts, call.top, call.intermediate = tokens, hidden, experts, top, intermediate
+    call.local_offset, call.local_experts = (0, 0) if window is None else window
+    call.renormalize = 1 if renormalize else 0
+    call.weight_dtype = 5 if f32 else 7 if mx else 6 if fp8 else 4
+    call.activation = activation
+    call.out, call.ids, call.weights, call.scores = out.ctypes.data, ids.ctypes.data, weights.ctypes.data, \
+        score_out.ctypes.data
+    threads = LIB.oracle_moe_layer_ex(ctypes.byref(call))
+    if scores:
+        return out, ids, weights, threads, score_out
     return out, ids, weights, threads

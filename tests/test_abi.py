@@ -111,6 +111,11 @@ def test_sort_refusals():
     call.local_offset, call.local_experts, call.experts = 0, 1 << 20, 1 << 20
     assert lib.uniserve_moe_sort(ctypes.byref(call), None) != 0
     assert "LDS" in message(call)
+    # The one-launch path keeps (3 + 16 waves) counters per local expert in 64 KB of LDS: 862 at
+    # most; more local experts (at any route count) are refused, never launched.
+    call.local_experts, call.experts, call.tokens, call.top = 863, 1100, 1024, 8
+    assert lib.uniserve_moe_sort(ctypes.byref(call), None) != 0
+    assert "LDS" in message(call)
     assert lib.uniserve_moe_sort(None, None) != 0
 
 
@@ -178,6 +183,18 @@ def test_layer_workspace_and_refusals():
     assert lib.uniserve_moe_layer_workspace(64, 2048, 128, 8, 768, abi.DTYPE["f16"]) == -1
     call = abi.LayerCall()
     assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "needs hidden" in message(call)
+    # The routing fields: a window outside the router's experts and an unknown gate are refused
+    # before anything launches (the pointers are never dereferenced).
+    p = 1 << 20
+    for name in ("hidden", "router", "up_gate", "down", "out", "workspace"):
+        setattr(call, name, p)
+    call.tokens, call.hidden_size, call.experts, call.top, call.intermediate = 64, 2048, 128, 8, 768
+    call.weight_dtype = abi.DTYPE["bf16"]
+    call.workspace_bytes = lib.uniserve_moe_layer_workspace(64, 2048, 128, 8, 768, abi.DTYPE["bf16"])
+    call.local_offset, call.local_experts = 100, 40
+    assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "window" in message(call)
+    call.local_offset, call.local_experts, call.activation = 0, 0, 2
+    assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "silu or gelu_tanh" in message(call)
 
 
 def test_sigmoid_gated_add_refusals():

@@ -10,8 +10,10 @@ agree within the reference's own bound, ``2 u terms`` relative to the largest ma
 (reference.rs:14-27, 66-69, 75-131). A wrong stacking order (gate before up), a wrong expert, a
 lost renormalisation or a wrong routing changes the rows by far more than that bound.
 
-CPU only: the fixture's widths (hidden 16, intermediate 8) are below the HIP kernels' 64-element
-steps, as they are below the reference's CUDA kernels' (their manifests refuse them too).
+The fixture's widths (hidden 16, intermediate 8) are below the HIP kernels' 64-element steps, as
+they are below the reference's CUDA kernels' (their manifests refuse them too); zero-padded to 64
+the blocks are unchanged (checked here on the oracle), and ``test_gpu_checkpoint.py`` runs them so
+on the device.
 """
 
 import json
@@ -187,6 +189,61 @@ def forward(ids, tensors, config, oracle):
         x = x + moe_block(rms_norm(x, w("post_attention_layernorm"), eps), tensors, prefix, config, oracle)
     hidden = rms_norm(x, w_all["model.norm.weight"], eps)
     return hidden, hidden @ w_all["lm_head.weight"].T
+
+
+# ---- the blocks at the kernels' widths ------------------------------------------------------------
+
+PAD = 64
+
+
+def block_inputs(ids, tensors, config, oracle):
+    """Each MoE block's input rows in the float64 forward of the fixture's model."""
+    w_all = {name: t.double().numpy() for name, t in tensors.items()}
+    eps = config["rms_norm_eps"]
+    x = w_all["model.embed_tokens.weight"][ids]
+    for layer in range(config["num_hidden_layers"]):
+        prefix = f"model.layers.{layer}"
+        w = lambda name, p=prefix: w_all[f"{p}.{name}.weight"] if f"{p}.{name}.weight" in w_all else w_all[f"{p}.{name}"]  # noqa: E731
+        x = x + attention(rms_norm(x, w("input_layernorm"), eps), w, config)
+        h = rms_norm(x, w("post_attention_layernorm"), eps)
+        yield layer, prefix, h
+        x = x + moe_block(h, tensors, prefix, config, oracle)
+
+
+def padded(up_gate, down, router, H, I):
+    """Zero-padded copies at hidden and intermediate PAD: up rows 0..I-1, gate rows PAD..PAD+I-1."""
+    E = up_gate.shape[0]
+    ug = torch.zeros((E, 2 * PAD, PAD), dtype=torch.float32)
+    ug[:, :I, :H] = up_gate[:, :I]
+    ug[:, PAD:PAD + I, :H] = up_gate[:, I:]
+    dn = torch.zeros((E, PAD, PAD), dtype=torch.float32)
+    dn[:, :H, :I] = down
+    rt = torch.zeros((E, PAD), dtype=torch.float32)
+    rt[:, :H] = router
+    return ug, dn, rt
+
+
+def test_zero_padded_blocks_are_the_checkpoint_s_blocks(fixture, oracle):
+    """The oracle's bf16 layer on the zero-padded stacks (hidden and intermediate 64, the HIP
+    layer's smallest) against each block of the float64 forward: padding adds nothing, so the
+    padded columns come out exactly zero and the rest within the bf16 bar (relative to the peak)."""
+    config, tensors, reference = fixture
+    E, top = config["num_experts"], config["num_experts_per_tok"]
+    H, I = config["hidden_size"], config["moe_intermediate_size"]
+    ids = reference["rows.0.ids"].numpy().astype(np.int64)
+    for layer, prefix, h in block_inputs(ids, tensors, config, oracle):
+        up_gate, down = (t.float() for t in stack_experts(dict(tensors), prefix, E))
+        ug, dn, rt = padded(up_gate, down, router_weight(tensors, prefix).float(), H, I)
+        x = np.zeros((h.shape[0], PAD), np.float32)
+        x[:, :H] = h
+        b = lambda a: oracle.bf16_encode(np.asarray(a, np.float32))  # noqa: E731
+        out, _, _, _ = oracle.moe_layer(b(x), b(rt.numpy()), b(ug.numpy()), b(dn.numpy()), top)
+        got = oracle.bf16_decode(out).astype(np.float64)
+        assert (got[:, H:] == 0).all()
+        want = moe_block(h, tensors, prefix, config, oracle)
+        peak = np.abs(want).max()
+        assert np.abs(got[:, :H] - want).max() <= 2e-2 * peak
+        assert np.abs(got[:, :H] - want).mean() <= 1e-3 * max(1.0, peak)
 
 
 def stack_terms(config, keys):

@@ -54,6 +54,8 @@ def quantized_stacks(device, experts, hidden, intermediate, seed=2):
     (64, 2048, 128, 8, 768, "uniform"), (1024, 2048, 128, 8, 768, "zipf"), (5, 4096, 16, 8, 1536, "uniform"),
     # the unsplit stream kernel with two 16-row blocks per pass, several passes on hot experts
     (256, 2048, 128, 8, 768, "zipf"),
+    # the two-workgroup e4m3 kernels at 235B width (BASELINE configs[4]'s H and I)
+    (1024, 4096, 128, 8, 1536, "zipf"),
     # prefill kernels at their smallest shapes: two K stages, one 256-column FC2 slice, ragged tiles
     (600, 256, 8, 2, 256, "zipf"),
     # the split stream kernel with two 16-row blocks per pass and, on the hottest expert, two passes
@@ -104,6 +106,8 @@ LAYERS = {
     "30b decode fp8": (64, 2048, 128, 8, 768, "f8e4m3", False, None),
     "30b prefill fp8 zipf": (8192, 2048, 128, 8, 768, "f8e4m3", True, 96),
     "235b decode fp8 one token": (1, 4096, 128, 8, 1536, "f8e4m3", False, None),
+    # the two-workgroup e4m3 kernels at 235B width, route-major scales
+    "235b prefill fp8 zipf": (4096, 4096, 128, 8, 1536, "f8e4m3", True, 64),
 }
 
 
@@ -142,10 +146,17 @@ def test_layer_against_the_oracle(device, case):
     x_bits = bf16_bits(x)[rows]
     router_bits = bf16_bits(router)
     if zipf:
-        # The bias enters the scores before their rounding; the oracle's router has no bias, so it
-        # is handed the device's own bf16 scores through a router of one-hot rows.
+        # The biased scores against the oracle's router (x . W^T + b in FP32, one rounding):
+        # the summation orders differ, so within one bf16 step, and nearly all bit for bit.
         scores = layer.view("scores", torch.bfloat16, (tokens, experts))
-        want_ids, _ = O.topk_softmax(bf16_bits(scores)[rows], top, score_kind=1)
+        score_bits = bf16_bits(scores)[rows]
+        want_scores = O.router_gemm(x_bits, router_bits, zipf_bias(experts))
+        s_got = O.bf16_decode(score_bits).astype(np.float64)
+        s_want = O.bf16_decode(want_scores).astype(np.float64)
+        assert (np.abs(s_got - s_want) <= 2.0**-7 * np.abs(s_want) + 1e-6).all()
+        assert (score_bits == want_scores).mean() > 0.99
+        # Routing is exact given the scores: the device's ids are the oracle's topk of them.
+        want_ids, _ = O.topk_softmax(score_bits, top, score_kind=1)
         np.testing.assert_array_equal(ids[rows], want_ids)
         hist = np.bincount(ids.ravel(), minlength=experts)
         assert hist[0] > 3 * hist[experts // 2], "the Zipf bias skews the routing"

@@ -183,6 +183,22 @@ def test_sort_is_bit_exact(device, tokens, top, experts, skew, live):
     assert_sort_equal(got, want, tokens, top)
 
 
+@pytest.mark.parametrize("tokens,top,experts,window,live", [
+    # The one-launch path (moe_sort_kernel): at most 4096 routes over more experts than the
+    # one-workgroup path keeps (> 512 local experts)...
+    (500, 8, 640, None, None), (512, 8, 1100, (100, 700), 500), (4096, 1, 860, None, 4000),
+    # ...and above 4096 routes over more local experts than the split path's chunks hold (> 1024);
+    # those need more LDS than a workgroup has, so the entry refuses them (tested on the CPU).
+])
+def test_sort_one_launch_path_is_bit_exact(device, tokens, top, experts, window, live):
+    announce("sort one-launch path", tokens, top, experts, window, live)
+    rng = np.random.default_rng(tokens + experts)
+    ids = rng.integers(0, experts, (tokens, top)).astype(np.int32)
+    local = None if window is None else (window[0], window[0] + window[1])
+    got, want = sort_both(device, ids, experts, local, live)
+    assert_sort_equal(got, want, tokens, top)
+
+
 def test_sort_of_a_window_with_out_of_range_ids(device):
     announce("sort window with foreign ids")
     rng = np.random.default_rng(9)

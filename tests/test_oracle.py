@@ -684,3 +684,147 @@ def test_mx_products_against_float64():
         for p in range(t * 128, t2l[t]):
             want = d2[t2e[t]] @ dg[p]
             np.testing.assert_allclose(products[p], want, rtol=1e-4, atol=1e-5 * np.abs(want).max())
+
+
+# ---- router bias, the gelu_tanh gate, the f32 path and the layer's routing options ---------------------
+
+
+def test_router_bias_enters_the_fp32_sum_before_the_one_rounding():
+    """Float64 brute force: bf16(x.W + b) within half a bf16 step of the exact value; and a crafted
+    case where rounding the product first and adding the bias after gives another bf16 value."""
+    rng = np.random.default_rng(3)
+    x = O.bf16_encode(rng.standard_normal((40, 256)).astype(np.float32))
+    w = O.bf16_encode((rng.standard_normal((24, 256)) * 0.02).astype(np.float32))
+    bias = (-1.1 * np.log(np.arange(24) + 1.0)).astype(np.float32)
+    got = O.bf16_decode(O.router_gemm(x, w, bias)).astype(np.float64)
+    exact = O.bf16_decode(x).astype(np.float64) @ O.bf16_decode(w).astype(np.float64).T + bias
+    magnitude = np.abs(O.bf16_decode(x).astype(np.float64)) @ np.abs(O.bf16_decode(w).astype(np.float64)).T
+    assert (np.abs(got - exact) <= np.abs(exact) * 2.0**-8 + 2.0**-22 * (magnitude + np.abs(bias))).all()
+    # x.W = 1 + 2^-9 (between two bf16 values, 1 and 1 + 2^-7, nearer 1), bias = 2^-8 + 2^-10:
+    # once-rounded bf16(1 + 2^-8 + 2^-9 + 2^-10) = 1 + 2^-7; rounded twice, bf16(1 + 2^-8 + 2^-10) = 1.
+    xs = O.bf16_encode(np.array([[1.0, 2.0**-9]], np.float32))
+    ws = O.bf16_encode(np.array([[1.0, 1.0]], np.float32))
+    once = O.bf16_decode(O.router_gemm(xs, ws, np.array([2.0**-8 + 2.0**-10], np.float32)))
+    assert once[0, 0] == 1.0 + 2.0**-7
+    assert O.bf16_decode(O.router_gemm(xs, ws))[0, 0] == 1.0  # the product alone rounds down
+    f32 = O.router_gemm_f32(O.bf16_decode(xs), O.bf16_decode(ws), np.array([2.0**-8 + 2.0**-10], np.float32))
+    assert f32[0, 0] == np.float32(1.0 + 2.0**-8 + 2.0**-9 + 2.0**-10)  # f32 scores: no rounding
+
+
+def test_gelu_tanh_gate_is_pytorch_s_tanh_approximation():
+    """crates/nn/src/functional/activation.rs:62-71: 0.5x(1 + tanh(sqrt(2/pi)(x + 0.044715x^3))),
+    checked against float64 and torch's gelu(approximate='tanh'); silu against float64."""
+    import torch
+
+    xs = np.concatenate([np.linspace(-12, 12, 2001), [0.0, -0.0, 1e-30, -1e-30, 30.0, -30.0]]).astype(np.float32)
+    got = np.array([O.gate_activation(float(v), 1) for v in xs], np.float64)
+    x64 = xs.astype(np.float64)
+    want = 0.5 * x64 * (1 + np.tanh(math.sqrt(2 / math.pi) * (x64 + 0.044715 * x64**3)))
+    # FP32 evaluation: a few ulps of the envelope |x| (1 + tanh cancels for large negative x).
+    envelope = 8 * 2.0**-24 * np.maximum(np.abs(x64), 2.0**-10)
+    assert (np.abs(got - want) <= envelope).all()
+    torch_values = torch.nn.functional.gelu(torch.from_numpy(xs), approximate="tanh").numpy().astype(np.float64)
+    assert (np.abs(got - torch_values) <= envelope).all()
+    got_silu = np.array([O.gate_activation(float(v), 0) for v in xs], np.float64)
+    assert (np.abs(got_silu - silu(x64)) <= 4 * 2.0**-24 * np.maximum(np.abs(silu(x64)), 2.0**-10)).all()
+    # The two gates are different functions (gelu_tanh(1) = 0.8412, silu(1) = 0.7311).
+    assert abs(O.gate_activation(1.0, 1) - 0.8411920) < 1e-6 and abs(O.gate_activation(1.0, 0) - 0.7310586) < 1e-6
+
+
+def tiny_layer_f32(seed=0):
+    """BASELINE configs[0] as stated: fp32, T=16, H=256, E=8, top-2, I=128; x ~ N(0,1), every weight
+    ~ N(0, 0.02), from seed 0 (the oracle's SplitMix64 -> Box-Muller normals)."""
+    T, H, E, K, I = 16, 256, 8, 2, 128
+    x = O.normal(T * H, seed * 10 + 1).reshape(T, H).astype(np.float32)
+    router = O.normal(E * H, seed * 10 + 2, 0.02).reshape(E, H).astype(np.float32)
+    up_gate = O.normal(E * 2 * I * H, seed * 10 + 3, 0.02).reshape(E, 2 * I, H).astype(np.float32)
+    down = O.normal(E * H * I, seed * 10 + 4, 0.02).reshape(E, H, I).astype(np.float32)
+    return x, router, up_gate, down, K
+
+
+def layer_by_hand(x, router, up_gate, down, top, bias=None, mapping=None, window=None, live=None,
+                  activation=0, score_round=None):
+    """MoE::routed in float64 from the reference's tests' definitions (route_by_hand,
+    expert_by_hand of crates/nn/tests/moe.rs:64-93, 367-377): each held route's weighted expert
+    output, summed; tokens past the live count give zero."""
+    x = np.asarray(x, np.float64)
+    scores = x @ np.asarray(router, np.float64).T
+    if bias is not None:
+        scores = scores + bias
+    if score_round is not None:
+        scores = score_round(scores)
+    ids, weights = route_by_hand(scores, top)
+    w1 = np.asarray(up_gate, np.float64)
+    w2 = np.asarray(down, np.float64)
+    I = w1.shape[1] // 2
+    offset, local = (0, w1.shape[0]) if window is None else window
+    out = np.zeros_like(x)
+    slots = ids if mapping is None else np.asarray(mapping)[ids]
+    for t in range(x.shape[0]):
+        if live is not None and t >= live:
+            continue
+        for k in range(top):
+            e = slots[t, k] - offset
+            if not 0 <= e < local:
+                continue
+            g = w1[e, I:] @ x[t]
+            gate = silu(g) if activation == 0 else 0.5 * g * (1 + np.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g**3)))
+            out[t] += weights[t, k] * (w2[e] @ (gate * (w1[e, :I] @ x[t])))
+    return out, slots, weights
+
+
+def test_f32_layer_is_the_float64_composition():
+    """configs[0] in fp32 (the CPU reference path rounds nothing): ids equal, weights and outputs
+    within the reference tests' FP32 tolerance (crates/nn/tests/moe.rs:29-30)."""
+    x, router, up_gate, down, top = tiny_layer_f32()
+    out, ids, weights, _, scores = O.moe_layer(x, router, up_gate, down, top, scores=True)
+    assert out.dtype == np.float32 and scores.dtype == np.float32
+    want, want_ids, want_weights = layer_by_hand(x, router, up_gate, down, top)
+    np.testing.assert_array_equal(ids, want_ids)
+    assert_close(weights, want_weights, F32_TOLERANCE)
+    assert_close(scores, x.astype(np.float64) @ router.astype(np.float64).T, F32_TOLERANCE)
+    assert_close(out, want, F32_TOLERANCE)
+    # gelu_tanh as the gate.
+    out_g, _, _, _ = O.moe_layer(x, router, up_gate, down, top, activation=1)
+    want_g, _, _ = layer_by_hand(x, router, up_gate, down, top, activation=1)
+    assert_close(out_g, want_g, F32_TOLERANCE)
+    assert np.abs(want_g - want).max() > 1e-3, "the gates differ on these inputs"
+
+
+def test_layer_routing_options_are_the_float64_composition():
+    """What MoE::routed passes beyond the rows (crates/nn/src/modules/moe.rs:650-671, 770-775): the
+    router bias, the slot map, the expert load of the live rows, the live count and the local
+    window - each against the float64 composition in bf16."""
+    T, H, E, K, I = 48, 256, 16, 4, 128
+    rng = np.random.default_rng(7)
+    x = O.bf16_encode(rng.standard_normal((T, H)).astype(np.float32))
+    router = O.bf16_encode((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    up_gate = O.bf16_encode((rng.standard_normal((E, 2 * I, H)) * 0.02).astype(np.float32))
+    down = O.bf16_encode((rng.standard_normal((E, H, I)) * 0.02).astype(np.float32))
+    bias = (-1.1 * np.log(np.arange(E) + 1.0)).astype(np.float32)
+    mapping = rng.permutation(E).astype(np.int32)
+    window = (4, 9)
+    live = 40
+    load = np.zeros(E, np.int64)
+    out, ids, weights, _, scores = O.moe_layer(
+        x, router, up_gate[4:13], down[4:13], K, router_bias=bias, mapping=mapping, load=load, live=live,
+        window=window, scores=True)
+    xf = O.bf16_decode(x).astype(np.float64)
+    rf = O.bf16_decode(router).astype(np.float64)
+    np.testing.assert_array_equal(scores, O.router_gemm(x, router, bias))
+    bf = lambda v: O.bf16_decode(O.bf16_encode(v.astype(np.float32))).astype(np.float64)  # noqa: E731
+    # Score rounding as the layer rounds (the float64 sum rounded once into bf16).
+    want, want_ids, want_weights = layer_by_hand(
+        xf, rf, O.bf16_decode(up_gate[4:13]), O.bf16_decode(down[4:13]), K, bias=bias, mapping=mapping,
+        window=window, live=live, score_round=bf)
+    np.testing.assert_array_equal(ids, want_ids)
+    assert_close(weights, want_weights, F32_TOLERANCE)
+    got = O.bf16_decode(out).astype(np.float64)
+    assert (got[live:] == 0).all()
+    rel = np.abs(got - want).max() / np.abs(want).max()
+    assert rel <= 2e-2 and np.abs(got - want).mean() <= 1e-3, rel
+    # The load counts every live route by its router expert (before the map).
+    unmapped = np.argsort(mapping)[ids[:live]]
+    np.testing.assert_array_equal(load, np.bincount(unmapped.ravel(), minlength=E))
+    # The bias skews the routing toward low router experts.
+    assert np.bincount(unmapped.ravel(), minlength=E)[:4].sum() > np.bincount(unmapped.ravel(), minlength=E)[-4:].sum()

@@ -262,7 +262,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
           for (int jb = 0; jb < 2; ++jb) {
             float g4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) g4[i] = silu(acc[tb][jb + 2][i]) * acc[tb][jb][i];
+            for (int i = 0; i < 4; ++i) g4[i] = gate(acc[tb][jb + 2][i], p.activation) * acc[tb][jb][i];
             parked[tb][jb] = uint2{pack_bf16x2(g4[0], g4[1]), pack_bf16x2(g4[2], g4[3])};
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[tb][jb][i] = acc[tb][jb + 2][i] = 0.0f;
@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
       for (int jb = 0; jb < 2; ++jb) {
         floatx4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + 2][i]) * acc[tb][jb][i];
+        for (int i = 0; i < 4; ++i) v[i] = gate(acc[tb][jb + 2][i], p.activation) * acc[tb][jb][i];
         uint2 packed;
         packed.x = pack_bf16x2(v[0], v[1]);
         packed.y = pack_bf16x2(v[2], v[3]);

@@ -71,6 +71,7 @@ struct GroupedFp8Params {
   float *out_code_scales;       ///< with out_codes: [permuted_rows, out_width / 128]
   int64_t scale_rows;           ///< nonzero (prefill kernel only): act_scales and out_code_scales are
                                 ///< route-major, [blocks, scale_rows] by permuted row
+  int32_t activation;           ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
 };
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
@@ -94,8 +95,9 @@ bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hid
 /// rows - instead of bf16 (refused unless fp8_fc1_quantizes).
 /// With `scale_rows` nonzero, hidden_scales are route-major ([hidden / 128, scale_rows] by permuted
 /// row, as launch_quantize_fp8_routes writes them) and so are the code scales written.
+/// `activation` is FC1's gate (uniserve_activation).
 int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales,
-                        int64_t scale_rows, void *stream);
+                        int64_t scale_rows, int32_t activation, void *stream);
 
 /// Whether the layer's two e4m3 products both run on the prefill kernel, so both can take
 /// route-major activation scales: one cache line holds 32 consecutive rows' scales of a block,

@@ -55,6 +55,7 @@ struct GroupedParams {
   int64_t n_total;          ///< weight rows per expert: 2I (FC1) or H (FC2)
   int64_t out_width;        ///< I (FC1) or H (FC2)
   int64_t top;
+  int32_t activation;       ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
 };
 
 __device__ __forceinline__ u32x4 load16(const uint16_t *pointer) {
@@ -202,7 +203,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
       if constexpr (kGated) {
         floatx4 h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        for (int i = 0; i < 4; ++i) h[i] = gate(acc[1][ms][i], p.activation) * acc[0][ms][i];
         store_bf16x4(row + n0 + 4 * g, h);
       } else {
         store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
@@ -323,7 +324,7 @@ __global__ void __launch_bounds__(kThreads) tiled_kernel(GroupedParams p) {
       for (int ni = 0; ni < 2; ++ni) {
         floatx4 h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = silu(acc[ni + 2][mi][i]) * acc[ni][mi][i];
+        for (int i = 0; i < 4; ++i) h[i] = gate(acc[ni + 2][mi][i], p.activation) * acc[ni][mi][i];
         store_bf16x4(row + slice + wn * 32 + ni * 16 + 4 * g, h);
       }
     } else {
@@ -354,6 +355,7 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
     q.n_total = p.n_total;
     q.out_width = p.out_width;
     q.top = p.top;
+    q.activation = p.activation;
     launch_prefill<prefill::Bf16, kGated>(q, max_tiles, s);
     return;
   }
@@ -367,8 +369,9 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
 }  // namespace
 }  // namespace uniserve
 
-extern "C" int32_t uniserve_gather_gemm(const uniserve_gather_call *call, void *stream) {
-  using namespace uniserve;
+namespace uniserve {
+
+int32_t gather_gemm_bf16(const uniserve_gather_call *call, int32_t activation, void *stream) {
   return guarded(call, [&]() -> int32_t {
     // The refusals of the reference entry (gather_gemm/cute_dsl/src/entry.cpp:18-42) and of
     // `GatherGemm::check` (crates/ops/src/moe/grouped.rs:250-324) the call's words can state.
@@ -409,12 +412,23 @@ extern "C" int32_t uniserve_gather_gemm(const uniserve_gather_call *call, void *
     p.n_total = call->width;
     p.out_width = call->width / 2;
     p.top = call->top;
+    p.activation = activation;
     const bool stream_path = call->tokens * call->top < kStreamRowsPerExpert * call->experts &&
                              call->hidden_size % 128 == 0;
     launch_grouped<true>(p, max_tiles, stream_path, call->tokens * call->top <= kOnePassRowsPerExpert * call->experts,
                          static_cast<hipStream_t>(stream));
     return launched(call, "gather_gemm");
   });
+}
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_gather_gemm(const uniserve_gather_call *call, void *stream) {
+  return uniserve::gather_gemm_bf16(call, UNISERVE_ACTIVATION_SILU, stream);
+}
+
+extern "C" int32_t uniserve_gather_gemm_gelu_tanh(const uniserve_gather_call *call, void *stream) {
+  return uniserve::gather_gemm_bf16(call, UNISERVE_ACTIVATION_GELU_TANH, stream);
 }
 
 extern "C" int32_t uniserve_route_gemm(const uniserve_route_call *call, void *stream) {

@@ -323,7 +323,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
       if constexpr (kGated) {
         floatx4 h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        for (int i = 0; i < 4; ++i) h[i] = gate(acc[1][ms][i], p.activation) * acc[0][ms][i];
         store_bf16x4(row + n0 + 4 * g, h);
       } else {
         store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
@@ -475,7 +475,7 @@ __global__ void __launch_bounds__(kThreads) tiled_fp8_kernel(GroupedFp8Params p)
       for (int ni = 0; ni < 2; ++ni) {
         floatx4 h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = silu(acc[ni + 2][mi][i]) * acc[ni][mi][i];
+        for (int i = 0; i < 4; ++i) h[i] = gate(acc[ni + 2][mi][i], p.activation) * acc[ni][mi][i];
         store_bf16x4(row + slice + wn * 32 + ni * 16 + 4 * g, h);
       }
     } else {
@@ -534,6 +534,7 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.n_total = p.n_total;
     q.out_width = p.out_width;
     q.top = p.top;
+    q.activation = p.activation;
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
     q.scale_rows = p.scale_rows;
@@ -606,7 +607,7 @@ bool fp8_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidd
 }
 
 int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, float *code_scales,
-                        int64_t scale_rows, void *stream) {
+                        int64_t scale_rows, int32_t activation, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_fp8 writes bf16 only");
     if (call->block_n != 128 || call->block_k != 128)
@@ -642,6 +643,7 @@ int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, fl
     p.n_total = call->width;
     p.out_width = call->width / 2;
     p.top = call->top;
+    p.activation = activation;
     if (codes != nullptr) {
       if (!fp8_fc1_quantizes(call->tokens, call->top, call->experts, call->hidden_size, call->width / 2))
         return UNISERVE_REFUSE(call, "gather_gemm_fp8 quantises its output only on the prefill kernel's shapes");
@@ -663,7 +665,11 @@ int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, fl
 }  // namespace uniserve
 
 extern "C" int32_t uniserve_gather_gemm_fp8(const uniserve_gather_fp8_call *call, void *stream) {
-  return uniserve::gather_gemm_fp8(call, nullptr, nullptr, 0, stream);
+  return uniserve::gather_gemm_fp8(call, nullptr, nullptr, 0, UNISERVE_ACTIVATION_SILU, stream);
+}
+
+extern "C" int32_t uniserve_gather_gemm_fp8_gelu_tanh(const uniserve_gather_fp8_call *call, void *stream) {
+  return uniserve::gather_gemm_fp8(call, nullptr, nullptr, 0, UNISERVE_ACTIVATION_GELU_TANH, stream);
 }
 
 extern "C" int32_t uniserve_route_gemm_fp8(const uniserve_route_fp8_call *call, void *stream) {

@@ -142,6 +142,7 @@ struct MxParams {
   int64_t as_stage;
   int64_t as_row;
   int32_t as_by_route;           ///< activation scale rows are permuted rows, not act rows
+  int32_t activation;            ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
 };
 
 /// Stride words of a scale table with `rows` rows in `layout`.
@@ -339,7 +340,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
       if constexpr (kGated) {
         floatx4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu(acc[1][ms][i]) * acc[0][ms][i];
+        for (int i = 0; i < 4; ++i) v[i] = gate(acc[1][ms][i], p.activation) * acc[0][ms][i];
         store_bf16x4(row + n0 + 4 * g, v);
       } else {
         store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
@@ -576,7 +577,7 @@ __global__ void __launch_bounds__(kWaves * kWave, 8 / kWaves) tiled_mx_kernel(Mx
       for (int jb = 0; jb < kBlocks / 2; ++jb) {
         floatx4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu(acc[tb][jb + kBlocks / 2][i]) * acc[tb][jb][i];
+        for (int i = 0; i < 4; ++i) v[i] = gate(acc[tb][jb + kBlocks / 2][i], p.activation) * acc[tb][jb][i];
         store_bf16x4(reinterpret_cast<uint16_t *>(row + (ww * kCols + jb * 16 + 4 * g) * 2), v);
       }
     } else {
@@ -682,7 +683,7 @@ bool mx_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidde
          !fp8_stream_path(routes_bound, experts) && tiled_fits(false, intermediate, hidden_size);
 }
 
-int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, void *stream) {
+int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, int32_t activation, void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_mx writes bf16 only");
     if (call->hidden == nullptr || call->hidden_scales == nullptr || call->weights == nullptr ||
@@ -720,6 +721,7 @@ int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, 
     p.n_total = call->width;
     p.out_width = call->width / 2;
     p.top = call->top;
+    p.activation = activation;
     scale_strides(call->weight_scale_layout, p.n_total, p.K, &p.ws_stage, &p.ws_row);
     scale_strides(scale_rows != 0 ? UNISERVE_MX_SCALES_STAGE_MAJOR : UNISERVE_MX_SCALES_ROW_MAJOR, scale_rows, p.K,
                   &p.as_stage, &p.as_row);
@@ -786,7 +788,11 @@ int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, vo
 }  // namespace uniserve
 
 extern "C" int32_t uniserve_gather_gemm_mx(const uniserve_gather_mx_call *call, void *stream) {
-  return uniserve::gather_gemm_mx(call, 0, stream);
+  return uniserve::gather_gemm_mx(call, 0, UNISERVE_ACTIVATION_SILU, stream);
+}
+
+extern "C" int32_t uniserve_gather_gemm_mx_gelu_tanh(const uniserve_gather_mx_call *call, void *stream) {
+  return uniserve::gather_gemm_mx(call, 0, UNISERVE_ACTIVATION_GELU_TANH, stream);
 }
 
 extern "C" int32_t uniserve_route_gemm_mx(const uniserve_route_mx_call *call, void *stream) {

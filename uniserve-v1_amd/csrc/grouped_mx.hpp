@@ -22,7 +22,7 @@ bool mx_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidde
 
 /// The product entries; with `scale_rows` nonzero the activation scales are stage-major by
 /// permuted row ([K / 128, scale_rows, 4], scale_rows >= permuted_rows).
-int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, void *stream);
+int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, int32_t activation, void *stream);
 int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, void *stream);
 
 }  // namespace uniserve

@@ -65,6 +65,7 @@ struct PrefillParams {
   float *out_code_scales;        ///< with out_codes: [permuted_rows, out_width / 128]
   int64_t scale_rows;            ///< nonzero: act_scales are [K / 128, scale_rows] and out_code_scales
                                  ///< [out_width / 128, scale_rows], both indexed by permuted row
+  int32_t activation;            ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
 };
 
 namespace prefill {
@@ -428,7 +429,7 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
       if constexpr (kGated) {
         float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = silu(acc[mi][1][4 * q + i]) * acc[mi][0][4 * q + i];
+        for (int i = 0; i < 4; ++i) v[i] = gate(acc[mi][1][4 * q + i], p.activation) * acc[mi][0][4 * q + i];
         uint2 packed;
         packed.x = pack_bf16x2(v[0], v[1]);
         packed.y = pack_bf16x2(v[2], v[3]);

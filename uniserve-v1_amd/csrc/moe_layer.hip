@@ -22,6 +22,10 @@
 #include "uniserve_route_gemm.h"
 #include "uniserve_topk_softmax.h"
 
+namespace uniserve {
+int32_t gather_gemm_bf16(const uniserve_gather_call *call, int32_t activation, void *stream);
+}
+
 namespace {
 
 constexpr int64_t kTile = 128;
@@ -158,7 +162,7 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   fc1.out_dtype = UNISERVE_DTYPE_BF16;
   fc1.multiprocessors = call->multiprocessors;
   fc1.weight_scale_layout = call->weight_scale_layout;
-  if (want(UNISERVE_MOE_LAYER_GATHER) && gather_gemm_mx(&fc1, scale_rows, stream) != 0)
+  if (want(UNISERVE_MOE_LAYER_GATHER) && gather_gemm_mx(&fc1, scale_rows, static_cast<int32_t>(call->activation), stream) != 0)
     return forward_error(call, "gather_gemm_mx", fc1);
 
   uniserve_quantize_mxfp8_call qg{};
@@ -227,8 +231,20 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (call->workspace_bytes < v.total)
       return UNISERVE_REFUSE(call, "moe_layer needs %lld workspace bytes, has %lld",
                              static_cast<long long>(v.total), static_cast<long long>(call->workspace_bytes));
+    if (call->activation != UNISERVE_ACTIVATION_SILU && call->activation != UNISERVE_ACTIVATION_GELU_TANH)
+      return UNISERVE_REFUSE(call, "moe_layer: FC1 gates with silu or gelu_tanh, not activation %lld",
+                             static_cast<long long>(call->activation));
+    // The window the stacks hold (the whole router when local_experts is 0). The products are
+    // told the router's expert count: they read it for their kernel choice only, and the views
+    // above were laid out with it (a window never needs more tiles than every expert).
+    const int64_t local_experts = call->local_experts == 0 ? call->experts : call->local_experts;
+    if (local_experts < 0 || call->local_offset < 0 || call->local_offset + local_experts > call->experts)
+      return UNISERVE_REFUSE(call, "moe_layer's expert window [%lld, %lld + %lld) lies outside the router's %lld experts",
+                             static_cast<long long>(call->local_offset), static_cast<long long>(call->local_offset),
+                             static_cast<long long>(local_experts), static_cast<long long>(call->experts));
     if (call->tokens == 0) return 0;
     if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
+    const int32_t activation = static_cast<int32_t>(call->activation);
 
     char *ws = static_cast<char *>(call->workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
@@ -256,12 +272,13 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     char message[512] = {0};
     if (want(UNISERVE_MOE_LAYER_TOPK) && uniserve_topk_softmax_launch(at(v.scores), 1, call->experts, static_cast<int32_t>(call->tokens),
                                      static_cast<int32_t>(call->experts), static_cast<int32_t>(call->top),
-                                     call->renormalize ? 1 : 0, nullptr, -1, ids, weights, nullptr,
-                                     reinterpret_cast<const uint32_t *>(call->live_tokens), nullptr, stream,
+                                     call->renormalize ? 1 : 0, nullptr, -1, ids, weights, call->map,
+                                     reinterpret_cast<const uint32_t *>(call->live_tokens),
+                                     call->load, stream,
                                      message, sizeof(message)) != 0)
       return UNISERVE_REFUSE(call, "topk_softmax: %s", message);
 
-    // 3. moe_sort over every expert.
+    // 3. moe_sort over the window's experts.
     uniserve_moe_sort_call sort{};
     sort.ids = ids;
     sort.scales = weights;
@@ -274,8 +291,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     sort.tokens = call->tokens;
     sort.top = call->top;
     sort.experts = call->experts;
-    sort.local_experts = call->experts;
-    sort.local_offset = 0;
+    sort.local_experts = local_experts;
+    sort.local_offset = call->local_offset;
     sort.tile_tokens = kTile;
     sort.scales_dtype = UNISERVE_DTYPE_F32;
     sort.live_tokens = call->live_tokens;
@@ -302,7 +319,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       fc1.top = call->top;
       fc1.dtype = UNISERVE_DTYPE_BF16;
       fc1.multiprocessors = call->multiprocessors;
-      if (want(UNISERVE_MOE_LAYER_GATHER) && uniserve_gather_gemm(&fc1, stream) != 0) return forward_error(call, "gather_gemm", fc1);
+      if (want(UNISERVE_MOE_LAYER_GATHER) && gather_gemm_bf16(&fc1, activation, stream) != 0) return forward_error(call, "gather_gemm", fc1);
 
       uniserve_route_call fc2{};
       fc2.rows = at(v.gated);
@@ -366,9 +383,9 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       } else if (fused) {
         // Prefill shapes: FC1 writes the gated rows straight in FC2's e4m3 form.
         if (gather_gemm_fp8(&fc1, static_cast<uint8_t *>(at(v.gated_q)), static_cast<float *>(at(v.gated_s)), scale_rows,
-                            stream) != 0)
+                            activation, stream) != 0)
           return forward_error(call, "gather_gemm_fp8", fc1);
-      } else if (uniserve_gather_gemm_fp8(&fc1, stream) != 0) {
+      } else if (gather_gemm_fp8(&fc1, nullptr, nullptr, 0, activation, stream) != 0) {
         return forward_error(call, "gather_gemm_fp8", fc1);
       }
 

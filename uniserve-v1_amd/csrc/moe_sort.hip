@@ -5,12 +5,20 @@
 // expert, each expert's routes in ascending expanded-route order from a tile boundary, and writes
 // the tile tables, the three maps and the two counts. Integer work, exact.
 //
-// One launch, no scratch memory. Workgroup b owns the chunk [b * kChunk, (b + 1) * kChunk) of the
-// routes and computes everything it needs itself:
+// Three paths, chosen by the route count R = tokens * top and the local expert count L; none uses
+// memory beyond the call's own outputs:
+//
+//   * small_sort_kernel (R <= 4096, L <= 512; decode): one workgroup reads `ids` once and keeps
+//     each wave's routes and match masks in registers from the count to the placement.
+//   * sort_count_kernel -> sort_scan_kernel -> sort_place_kernel (R > 4096, L <= 1024; prefill):
+//     three launches over 2048-route chunks; the count parks each chunk's per-expert counts in the
+//     chunk's own stretch of `expanded_to_permuted`, which only that chunk's placement overwrites.
+//   * moe_sort_kernel (the rest: R <= 4096 with 512 < L <= 862; L is capped by 19 counters per
+//     expert in 64 KB of LDS, larger windows are refused): one launch; workgroup b owns the chunk
+//     [b * kChunk, (b + 1) * kChunk) of the routes and computes everything it needs itself:
 //
 //   1. count every held route by expert (the totals) and those before its chunk (its base within
-//      each expert), reading the whole `ids` vector - a few hundred KB from L2 even at 8192 tokens
-//      x 8, cheaper than a second launch and a global barrier;
+//      each expert), reading the whole `ids` vector;
 //   2. the tiles per expert and their exclusive scan (workgroup 0 also writes the tile tables, the
 //      padding rows and the counts);
 //   3. place its chunk: each wavefront owns a contiguous slice, counts it per expert, a scan over

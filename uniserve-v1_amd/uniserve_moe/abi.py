@@ -10,6 +10,10 @@ import os
 from pathlib import Path
 
 #: ``uniserve_dtype`` (crates/ops/src/abi.rs:79-92).
+# FC1's gate (uniserve_activation); the FC1 entries take it by name, the layer call as a field.
+ACTIVATION = {"silu": 0, "gelu_tanh": 1}
+ENTRY_SUFFIX = {"silu": "", "gelu_tanh": "_gelu_tanh"}
+
 DTYPE = {
     "u8": 0,
     "i32": 1,
@@ -311,6 +315,11 @@ class LayerCall(ctypes.Structure):
         ("multiprocessors", _I64),
         ("weight_scale_layout", _I64),
         ("error", _ERR),
+        ("map", _P),
+        ("load", _P),
+        ("local_offset", _I64),
+        ("local_experts", _I64),
+        ("activation", _I64),
     ]
 
 
@@ -376,15 +385,18 @@ _LIBRARY = None
 _ENTRIES = {
     "uniserve_moe_sort": SortCall,
     "uniserve_gather_gemm": GatherCall,
+    "uniserve_gather_gemm_gelu_tanh": GatherCall,
     "uniserve_route_gemm": RouteCall,
     "uniserve_moe_unpermute": UnpermuteCall,
     "uniserve_gemm": GemmCall,
     "uniserve_quantize_fp8": QuantizeFp8Call,
     "uniserve_gather_gemm_fp8": GatherFp8Call,
+    "uniserve_gather_gemm_fp8_gelu_tanh": GatherFp8Call,
     "uniserve_route_gemm_fp8": RouteFp8Call,
     "uniserve_moe_layer": LayerCall,
     "uniserve_quantize_mxfp8": QuantizeMxfp8Call,
     "uniserve_gather_gemm_mx": GatherMxCall,
+    "uniserve_gather_gemm_mx_gelu_tanh": GatherMxCall,
     "uniserve_route_gemm_mx": RouteMxCall,
     "uniserve_mx_stage_major_scales": MxStageScalesCall,
 }

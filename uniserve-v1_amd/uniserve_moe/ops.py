@@ -12,7 +12,9 @@ import ctypes
 import torch
 
 from .abi import (
+    ACTIVATION,
     DTYPE,
+    ENTRY_SUFFIX,
     LAYOUT_PERMUTED,
     GatherCall,
     GatherFp8Call,
@@ -134,8 +136,9 @@ def permuted_rows(tokens, top, local_experts):
     return max_tiles(tokens, top, local_experts, TILE) * TILE
 
 
-def gather_gemm(hidden, up_gate, top, maps, rows, out=None):
-    """``functional::gather_gemm`` (moe.rs:476-636): ``[rows, I]`` gated products (bf16)."""
+def gather_gemm(hidden, up_gate, top, maps, rows, out=None, activation="silu"):
+    """``functional::gather_gemm`` (moe.rs:476-636): ``[rows, I]`` gated products (bf16), gated by
+    ``activation`` ("silu" or "gelu_tanh": the entry of that name)."""
     tokens, width = hidden.shape
     experts, gated, _ = up_gate.shape
     if out is None:
@@ -149,7 +152,8 @@ def gather_gemm(hidden, up_gate, top, maps, rows, out=None):
     call.tokens, call.permuted_rows, call.width, call.hidden_size = tokens, rows, gated, width
     call.experts, call.top, call.dtype = experts, top, DTYPE[_TORCH_DTYPE[hidden.dtype]]
     call.multiprocessors = multiprocessors(hidden.device)
-    _check(library().uniserve_gather_gemm(ctypes.byref(call), _stream(hidden.device)), call, "gather_gemm")
+    entry = getattr(library(), "uniserve_gather_gemm" + ENTRY_SUFFIX[activation])
+    _check(entry(ctypes.byref(call), _stream(hidden.device)), call, "gather_gemm")
     return out
 
 
@@ -220,7 +224,7 @@ def quantize_fp8(rows_tensor, row_limit=None):
     return out, scales
 
 
-def gather_gemm_fp8(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None):
+def gather_gemm_fp8(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None, activation="silu"):
     tokens, width = hidden_q.shape
     experts, gated, _ = up_gate_q.shape
     if out is None:
@@ -235,7 +239,8 @@ def gather_gemm_fp8(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, o
     call.tokens, call.permuted_rows, call.width, call.hidden_size = tokens, rows, gated, width
     call.experts, call.top, call.block_n, call.block_k = experts, top, 128, 128
     call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(hidden_q.device)
-    _check(library().uniserve_gather_gemm_fp8(ctypes.byref(call), _stream(hidden_q.device)), call, "gather_gemm_fp8")
+    entry = getattr(library(), "uniserve_gather_gemm_fp8" + ENTRY_SUFFIX[activation])
+    _check(entry(ctypes.byref(call), _stream(hidden_q.device)), call, "gather_gemm_fp8")
     return out
 
 
@@ -288,7 +293,8 @@ def mx_stage_major_scales(scales):
     return out
 
 
-def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None, scale_layout="row"):
+def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, out=None, scale_layout="row",
+                   activation="silu"):
     """FC1 over MXFP8 tokens and MXFP4 weights (``up_gate_q`` [E, 2I, H / 2] E2M1 pairs; the weight
     scales in ``scale_layout``, "row" or "stage")."""
     tokens, width = hidden_q.shape
@@ -306,7 +312,8 @@ def gather_gemm_mx(hidden_q, hidden_s, up_gate_q, up_gate_s, top, maps, rows, ou
     call.experts, call.top = experts, top
     call.out_dtype, call.multiprocessors = DTYPE["bf16"], multiprocessors(hidden_q.device)
     call.weight_scale_layout = MX_SCALE_LAYOUTS[scale_layout]
-    _check(library().uniserve_gather_gemm_mx(ctypes.byref(call), _stream(hidden_q.device)), call, "gather_gemm_mx")
+    entry = getattr(library(), "uniserve_gather_gemm_mx" + ENTRY_SUFFIX[activation])
+    _check(entry(ctypes.byref(call), _stream(hidden_q.device)), call, "gather_gemm_mx")
     return out
 
 
@@ -364,7 +371,11 @@ class MoeLayer:
         return self.workspace[offset:offset + count * size].view(dtype).view(*shape)
 
     def __call__(self, hidden, router, up_gate, down, out=None, up_gate_scales=None, down_scales=None,
-                 router_bias=None, live_tokens=None, scale_layout="row"):
+                 router_bias=None, live_tokens=None, scale_layout="row", mapping=None, load=None, window=None,
+                 activation="silu"):
+        """``mapping`` (int32 [experts]) names each router expert's slot, ``load`` (int64 [experts])
+        counts the live routes by router expert, ``window`` = (local_offset, local_experts) names
+        the slots the stacks hold (``up_gate`` [local_experts, ...]); ``activation`` is FC1's gate."""
         tokens = hidden.shape[0]
         if tokens != self.max_tokens:
             raise ValueError("the layer's workspace is laid out for its max_tokens")
@@ -383,6 +394,9 @@ class MoeLayer:
         call.weight_dtype = DTYPE[self.weight_dtype]
         call.multiprocessors = multiprocessors(hidden.device)
         call.weight_scale_layout = MX_SCALE_LAYOUTS[scale_layout]
+        call.map, call.load = _ptr(mapping), _ptr(load)
+        call.local_offset, call.local_experts = (0, 0) if window is None else window
+        call.activation = ACTIVATION[activation]
         _check(library().uniserve_moe_layer(ctypes.byref(call), _stream(hidden.device)), call, "moe_layer")
         return out
 
