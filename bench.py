@@ -49,6 +49,9 @@ def parse():
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--config", default="30b-decode-bf16", choices=sorted(CONFIGS))
     parser.add_argument("--extra", action="store_true", help="also measure every other BASELINE config")
+    parser.add_argument("--also", default="30b-prefill-fp8",
+                        help="comma-separated configs measured briefly beside the main one (default: the fp8 "
+                             "prefill target's config); '' for none")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     parser.add_argument("--cpu-runs", type=int, default=3)
     parser.add_argument("--traffic-summary", metavar="DIR",
@@ -357,14 +360,18 @@ def main():
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),
     }
-    if args.extra:
-        extra = {}
-        for name in CONFIGS:
-            if name == args.config:
-                continue
-            _, ms, tps, roof, lay, _ = run_config(name, max(10, args.steps // 10), max(3, args.warmup // 4), False, 0)
-            extra[name] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(tps, 1), "roofline": roof, "layer": lay}
-            torch.cuda.empty_cache()
+    others = list(CONFIGS) if args.extra else [name for name in args.also.split(",") if name]
+    extra = {}
+    for name in others:
+        if name == args.config:
+            continue
+        if name not in CONFIGS:
+            raise SystemExit(f"unknown config {name!r}")
+        del w
+        torch.cuda.empty_cache()
+        w, ms, tps, roof, lay, _ = run_config(name, max(10, args.steps // 10), max(3, args.warmup // 4), False, 0)
+        extra[name] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(tps, 1), "roofline": roof, "layer": lay}
+    if extra:
         line["extra"] = extra
     print(json.dumps(line))
 

@@ -50,7 +50,9 @@ struct uniserve_moe_layer_call {
   int64_t activation;          ///< FC1's gate: uniserve_activation (0 = silu)
 };
 
-/// Workspace bytes the call needs for these extents, or -1 for extents it does not serve.
+/// Workspace bytes the call needs for these extents, or -1 for extents it does not serve. The
+/// workspace's first 1024 bytes (the `ticket` view) must be zero before the first call that uses
+/// it; every call leaves them zero (the rest needs no initialisation).
 UNISERVE_EXTERN_C int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_size,
                                                        int64_t experts, int64_t top,
                                                        int64_t intermediate, int64_t weight_dtype);
@@ -58,6 +60,7 @@ UNISERVE_EXTERN_C int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t h
 /// Offsets (bytes from `workspace`) of the intermediate tensors, for callers that read them:
 /// scores, ids, weights, the seven sort maps, gated rows, products.
 struct uniserve_moe_layer_views {
+  int64_t ticket;              ///< [256] u32 counters of the fused decode front end (offset 0)
   int64_t scores;              ///< [tokens, experts] bf16
   int64_t ids;                 ///< [tokens, top] i32
   int64_t weights;             ///< [tokens, top] f32
@@ -96,7 +99,9 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_views_of(int64_t tokens, int64_t hi
 UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_call *call, void *stream);
 
 /// The layer's launches in order; the quantiser steps launch nothing for bf16 weights, and
-/// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised.
+/// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised. At decode
+/// sizes (at most 4096 routes over at most 512 local experts, a router of at most 1024 experts)
+/// ROUTER launches the router, topk and sort as one kernel, and TOPK and SORT launch nothing.
 enum uniserve_moe_layer_step {
   UNISERVE_MOE_LAYER_ROUTER = 0,
   UNISERVE_MOE_LAYER_TOPK = 1,

@@ -109,6 +109,13 @@ float oracle_f32_from_e4m3(uint8_t code) {
   return (code & 0x80) ? -magnitude : magnitude;
 }
 
+/* The 256 e4m3 values, decoded once when the library loads (the products read them per element). */
+static float e4m3_values[256];
+
+__attribute__((constructor)) static void fill_e4m3_values(void) {
+  for (int code = 0; code < 256; ++code) e4m3_values[code] = oracle_f32_from_e4m3((uint8_t)code);
+}
+
 void oracle_bf16_encode(const float *in, uint16_t *out, int64_t count) {
   for (int64_t i = 0; i < count; ++i) out[i] = oracle_bf16_from_f32(in[i]);
 }
@@ -680,7 +687,7 @@ static float dot_fp8(const uint8_t *a, const float *sa, const uint8_t *b, const 
   for (int64_t kb = 0; kb < k / block; ++kb) {
     float partial = 0.0f;
     for (int64_t i = 0; i < block; ++i)
-      partial += oracle_f32_from_e4m3(a[kb * block + i]) * oracle_f32_from_e4m3(b[kb * block + i]);
+      partial += e4m3_values[a[kb * block + i]] * e4m3_values[b[kb * block + i]];
     total += partial * (sa[kb] * sb[kb]);
   }
   return total;
@@ -846,7 +853,7 @@ static float dot_mx(const uint8_t *a, const uint8_t *sa, const uint8_t *w, const
     for (int64_t i = 0; i < 32; ++i) {
       const int64_t at = b * 32 + i;
       const uint8_t code = (uint8_t)((w[at / 2] >> (4 * (at & 1))) & 15);
-      partial += oracle_f32_from_e4m3(a[at]) * oracle_f32_from_e2m1(code);
+      partial += e4m3_values[a[at]] * oracle_f32_from_e2m1(code);
     }
     total += partial * (mx_power(sa[b]) * mx_power(sw[b]));
   }

@@ -13,6 +13,14 @@
 
 #include "uniserve_abi.h"
 
+// Probe points of latency-bound routines (a build with UNISERVE_FRONT_TRACE records timestamps at
+// them; the product build compiles them to nothing).
+#ifndef UNISERVE_TRACE
+#define UNISERVE_TRACE(slot) \
+  do {                       \
+  } while (0)
+#endif
+
 namespace uniserve {
 
 constexpr int kWave = 64;

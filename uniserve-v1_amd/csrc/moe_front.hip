@@ -1,0 +1,154 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The MoE layer's front end at decode sizes in one launch: the router scores
+// (crates/nn/src/modules/moe.rs:656-671), topk_softmax (crates/ops/src/moe/routing.rs) and
+// moe_sort (crates/ops/src/moe/sort.rs) - what MoE::routed issues as three launches
+// (moe.rs:770-775), each of which at 64 tokens is a few microseconds of latency and little work.
+//
+// Every workgroup computes one 16-token x 16-expert tile of scores, its contraction split over 16
+// wavefronts (partial sums added in wavefront order, the bias added to the FP32 sum, one rounding
+// into bf16), and stores it. Then two rounds of tickets - agent-scope atomic counters with
+// release/acquire ordering, so a taker of a round's last ticket sees everything the round's
+// other workgroups stored:
+//   * the last of a token block's workgroups routes that block's 16 tokens (the topk routine of
+//     topk_route.hpp, one token per 32-lane half: ids and weights bit for bit those of the
+//     topk_softmax kernel) - the routing is spread over the token blocks' CUs, since on one CU its
+//     VALU work is the front end's longest step;
+//   * the last of the token blocks sorts every route (the one-workgroup sort of sort_small.hpp:
+//     every map entry the layer reads bit for bit the moe_sort entry's; the padding rows of the two
+//     permuted maps, which the layer never reads, are not written).
+// Each last taker resets its counter, so every launch leaves the counters zero.
+#ifdef UNISERVE_FRONT_TRACE
+#include <hip/hip_runtime.h>
+__device__ unsigned long long front_trace[64];
+#define UNISERVE_TRACE(slot)                                                                      \
+  do {                                                                                            \
+    if (threadIdx.x == 0) front_trace[slot] = __builtin_amdgcn_s_memrealtime();                   \
+  } while (0)
+extern "C" int uniserve_front_trace_read(unsigned long long *out) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(front_trace), sizeof(front_trace)) == hipSuccess ? 0 : 1;
+}
+#endif
+#include "common.hpp"
+#include "moe_front.hpp"
+#include "sort_small.hpp"
+#include "topk_route.hpp"
+
+namespace uniserve {
+namespace {
+
+constexpr int kThreads = sort::kSortThreads;  // the sort's workgroup: 16 wavefronts
+constexpr int kWaves = kThreads / kWave;
+constexpr int kUnroll = 4;                    // K steps of 32 whose loads a wavefront keeps in flight
+constexpr int kTile = 16;
+
+/// Takes a ticket of `counter` for one of `takers` workgroups (thread 0; the workgroup's stores
+/// ordered before it by the caller's barrier); answers, to every thread, whether it was the last,
+/// and then the counter is reset and every taker's stores are visible to this workgroup.
+__device__ __forceinline__ bool last_ticket(uint32_t *counter, uint32_t takers, int32_t *flag) {
+  if (threadIdx.x == 0) {
+    const uint32_t taken = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = taken + 1 == takers;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (*flag == 0) return false;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return true;
+}
+
+__global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
+  extern __shared__ __align__(16) int32_t front_lds[];
+  __shared__ int32_t flag;
+  if (blockIdx.x == 0 && blockIdx.y == 0) UNISERVE_TRACE(0);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+
+  // 1. One tile of scores. Lane l: token row l % 16 (operand B) and expert row l % 16 (operand A),
+  // eight K elements at 8 (l / 16); rows past the edge read row 0 and are never stored.
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * kTile + r16;
+  const int64_t n = static_cast<int64_t>(blockIdx.y) * kTile + r16;
+  const uint16_t *x_row = p.x + (m < p.tokens ? m : 0) * p.hidden + g * 8;
+  const uint16_t *w_row = p.w + (n < p.experts ? n : 0) * p.hidden + g * 8;
+  floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t steps = p.hidden / 32;
+  for (int64_t s = wave; s < steps; s += kWaves * kUnroll) {
+    u32x4 xv[kUnroll], wv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t step = s + u * kWaves;
+      if (step < steps) {
+        xv[u] = *reinterpret_cast<const u32x4 *>(x_row + step * 32);
+        wv[u] = *reinterpret_cast<const u32x4 *>(w_row + step * 32);
+      } else {
+        xv[u] = u32x4{0, 0, 0, 0};
+        wv[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc = mfma_16x16x32_bf16(wv[u], xv[u], acc);
+  }
+  floatx4 *partial = reinterpret_cast<floatx4 *>(front_lds);
+  partial[wave * kWave + lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    floatx4 total = partial[lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) total += partial[w * kWave + lane];
+    // Lane l holds token l % 16 and experts 4 (l / 16) .. + 3 of the tile.
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kTile + r16;
+    const int64_t col = static_cast<int64_t>(blockIdx.y) * kTile + 4 * g;
+    if (row < p.tokens) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (col + i >= p.experts) continue;
+        float v = total[i];
+        if (p.bias != nullptr) v += p.bias[col + i];
+        p.scores[row * p.experts + col + i] = f32_to_bf16(v);
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. The last of the token block's tiles routes its tokens, one per 32-lane half.
+  if (!last_ticket(p.ticket + 1 + blockIdx.x, gridDim.y, &flag)) return;
+  UNISERVE_TRACE(1);
+  const int half = static_cast<int>(threadIdx.x) / topk::kHalf;
+  if (half < kTile) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kTile + half;
+    const bool active = row < p.tokens;
+    topk::route_token(p.scores, 1, p.experts, static_cast<int>(active ? row : 0), static_cast<int>(p.experts), p.top,
+                      p.renormalize, nullptr, -1, p.ids, p.weights, p.map, p.live, p.load, active);
+  }
+  __syncthreads();
+  UNISERVE_TRACE(2);
+
+  // 3. The last of the token blocks sorts every route.
+  if (!last_ticket(p.ticket, gridDim.x, &flag)) return;
+  UNISERVE_TRACE(4);
+  sort::small_sort<false>(p.sort, front_lds);
+  UNISERVE_TRACE(3);
+}
+
+}  // namespace
+
+bool front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top, int64_t local_experts) {
+  const int64_t wide_tiles = ceil_div<int64_t>(tokens, 64) * ceil_div<int64_t>(experts, 64);
+  return tokens > 0 && ceil_div<int64_t>(tokens, kTile) <= kFrontTokenBlocks && wide_tiles < 64 &&
+         hidden % 32 == 0 && experts <= 1024 && top >= 1 && top <= 32 && top <= experts &&
+         tokens * top <= sort::kChunk && local_experts >= 1 && local_experts <= sort::kSmallMaxExperts;
+}
+
+void launch_front(const FrontParams &p, hipStream_t stream) {
+  const int64_t router_bytes = static_cast<int64_t>(kThreads) * sizeof(floatx4);
+  const int64_t sort_bytes = sort::small_sort_lds_words(p.sort.local_experts) * static_cast<int64_t>(sizeof(int32_t));
+  const size_t lds = static_cast<size_t>(router_bytes > sort_bytes ? router_bytes : sort_bytes);
+  const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.tokens, kTile)),
+                  static_cast<uint32_t>(ceil_div<int64_t>(p.experts, kTile)));
+  hipLaunchKernelGGL(front_kernel, grid, dim3(kThreads), lds, stream, p);
+}
+
+}  // namespace uniserve

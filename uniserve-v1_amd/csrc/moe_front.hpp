@@ -1,0 +1,43 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The layer's fused front end at decode sizes: router scores, topk_softmax and moe_sort in one
+// launch (moe_front.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "sort_small.hpp"
+
+namespace uniserve {
+
+/// Token blocks (16 tokens each) the front end's counters cover: one counter per block and one for
+/// the sort, kFrontTicketBytes in all.
+constexpr int64_t kFrontTokenBlocks = 255;
+constexpr int64_t kFrontTicketBytes = (1 + kFrontTokenBlocks) * 4;
+
+struct FrontParams {
+  const uint16_t *x;        ///< [tokens, hidden] bf16
+  const uint16_t *w;        ///< [experts, hidden] bf16 router
+  const float *bias;        ///< [experts] or null
+  uint16_t *scores;         ///< [tokens, experts] bf16
+  int64_t tokens, experts, hidden;
+  int32_t top, renormalize;
+  const int32_t *map;       ///< [experts] or null
+  const int32_t *live;      ///< [1] or null
+  unsigned long long *load; ///< [experts] or null
+  int32_t *ids;             ///< [tokens, top]
+  float *weights;           ///< [tokens, top]
+  uint32_t *ticket;         ///< [1 + kFrontTokenBlocks] counters, zero before the launch and after it
+  sort::SortParams sort;    ///< the sort over `ids` (its ids pointer is `ids`)
+};
+
+/// Whether one launch serves these extents: the router's split-contraction tiles, a router of at
+/// most 1024 experts picking at most 32, and a sort one workgroup does (<= 4096 routes over
+/// <= 512 local experts).
+bool front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top, int64_t local_experts);
+
+void launch_front(const FrontParams &p, hipStream_t stream);
+
+}  // namespace uniserve

@@ -12,6 +12,7 @@
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_mx.hpp"
+#include "moe_front.hpp"
 #include "router_gemm.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_moe_fp8.h"
@@ -48,6 +49,7 @@ bool views_of(int64_t tokens, int64_t hidden, int64_t experts, int64_t top, int6
     at += aligned(bytes > 0 ? bytes : 1);
     return here;
   };
+  v->ticket = take(uniserve::kFrontTicketBytes);  // first: the words a caller zeroes before a workspace's first call
   v->scores = take(tokens * experts * 2);
   v->ids = take(tokens * top * 4);
   v->weights = take(tokens * top * 4);
@@ -205,13 +207,15 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   return 0;
 }
 
-/// The layer's launches, all of them (`only` < 0) or the one step `only`.
-int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *stream) {
+/// The layer's launches, all of them (`only` < 0) or the one step `only`, over the workspace
+/// `workspace` of `workspace_bytes`.
+int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *stream, void *workspace,
+                  int64_t workspace_bytes) {
   using namespace uniserve;
   auto want = [&](int32_t step) { return only < 0 || only == step; };
   return guarded(call, [&]() -> int32_t {
     if (call->hidden == nullptr || call->router == nullptr || call->up_gate == nullptr ||
-        call->down == nullptr || call->out == nullptr || call->workspace == nullptr)
+        call->down == nullptr || call->out == nullptr || workspace == nullptr)
       return UNISERVE_REFUSE(call, "moe_layer needs hidden, router, both stacks, out and a workspace");
     const bool fp8 = call->weight_dtype == UNISERVE_DTYPE_F8E4M3;
     const bool mx = call->weight_dtype == UNISERVE_DTYPE_F4E2M1;
@@ -222,15 +226,15 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       return UNISERVE_REFUSE(call, "moe_layer: no MX scale layout %lld", static_cast<long long>(call->weight_scale_layout));
     if (mx && (call->hidden_size % 256 != 0 || call->intermediate % 256 != 0))
       return UNISERVE_REFUSE(call, "moe_layer: MXFP4 stacks need hidden and intermediate sizes of whole 256-element chunks");
-    if (reinterpret_cast<uintptr_t>(call->workspace) % kAlign != 0)
+    if (reinterpret_cast<uintptr_t>(workspace) % kAlign != 0)
       return UNISERVE_REFUSE(call, "moe_layer needs a 256-byte aligned workspace");
     uniserve_moe_layer_views v;
     if (!views_of(call->tokens, call->hidden_size, call->experts, call->top, call->intermediate,
                   call->weight_dtype, &v))
       return UNISERVE_REFUSE(call, "moe_layer does not serve these extents or this weight type");
-    if (call->workspace_bytes < v.total)
+    if (workspace_bytes < v.total)
       return UNISERVE_REFUSE(call, "moe_layer needs %lld workspace bytes, has %lld",
-                             static_cast<long long>(v.total), static_cast<long long>(call->workspace_bytes));
+                             static_cast<long long>(v.total), static_cast<long long>(workspace_bytes));
     if (call->activation != UNISERVE_ACTIVATION_SILU && call->activation != UNISERVE_ACTIVATION_GELU_TANH)
       return UNISERVE_REFUSE(call, "moe_layer: FC1 gates with silu or gelu_tanh, not activation %lld",
                              static_cast<long long>(call->activation));
@@ -246,7 +250,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
     const int32_t activation = static_cast<int32_t>(call->activation);
 
-    char *ws = static_cast<char *>(call->workspace);
+    char *ws = static_cast<char *>(workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
     const hipStream_t s = static_cast<hipStream_t>(stream);
     int32_t *ids = static_cast<int32_t *>(at(v.ids));
@@ -259,6 +263,48 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     int32_t *padded = static_cast<int32_t *>(at(v.total_padded_tokens));
     int32_t *tiles = static_cast<int32_t *>(at(v.num_non_exiting_tiles));
 
+    // Decode sizes: router, topk and sort in one launch (at the ROUTER step; TOPK and SORT launch
+    // nothing).
+    if (front_fits(call->tokens, call->experts, call->hidden_size, call->top, local_experts)) {
+      if (want(UNISERVE_MOE_LAYER_ROUTER)) {
+        FrontParams fp{};
+        fp.x = static_cast<const uint16_t *>(call->hidden);
+        fp.w = static_cast<const uint16_t *>(call->router);
+        fp.bias = call->router_bias;
+        fp.scores = static_cast<uint16_t *>(at(v.scores));
+        fp.tokens = call->tokens;
+        fp.experts = call->experts;
+        fp.hidden = call->hidden_size;
+        fp.top = static_cast<int32_t>(call->top);
+        fp.renormalize = call->renormalize ? 1 : 0;
+        fp.map = call->map;
+        fp.live = call->live_tokens;
+        fp.load = reinterpret_cast<unsigned long long *>(call->load);
+        fp.ids = ids;
+        fp.weights = weights;
+        fp.ticket = static_cast<uint32_t *>(at(v.ticket));
+        sort::SortParams &sp = fp.sort;
+        sp.ids = ids;
+        sp.tile_to_expert = t2e;
+        sp.tile_to_limit = t2l;
+        sp.expanded_to_permuted = e2p;
+        sp.permuted_to_expanded = p2e;
+        sp.permuted_to_token = p2t;
+        sp.total_padded_tokens = padded;
+        sp.num_non_exiting_tiles = tiles;
+        sp.live_tokens = call->live_tokens;
+        sp.routes = call->tokens * call->top;
+        sp.top = call->top;
+        sp.local_experts = static_cast<int32_t>(local_experts);
+        sp.local_offset = static_cast<int32_t>(call->local_offset);
+        sp.tile = static_cast<int32_t>(kTile);
+        int bits = 0;
+        while ((1ll << bits) <= local_experts) ++bits;
+        sp.key_bits = bits;
+        launch_front(fp, s);
+        if (int32_t status = launched(call, "router, topk and sort")) return status;
+      }
+    } else {
     // 1. Router scores, bf16 (the router Linear's output dtype).
     RouterParams rp{static_cast<const uint16_t *>(call->hidden), static_cast<const uint16_t *>(call->router),
                     static_cast<uint16_t *>(at(v.scores)), call->router_bias, call->tokens, call->experts,
@@ -298,6 +344,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     sort.live_tokens = call->live_tokens;
     sort.permuted_to_token = p2t;
     if (want(UNISERVE_MOE_LAYER_SORT) && uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
+    }
 
     // 4-5. The two products.
     if (mx) {
@@ -443,11 +490,13 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
 }  // namespace
 
 extern "C" int32_t uniserve_moe_layer(const uniserve_moe_layer_call *call, void *stream) {
-  return run_layer(call, -1, stream);
+  if (call == nullptr) return 1;
+  return run_layer(call, -1, stream, call->workspace, call->workspace_bytes);
 }
 
 extern "C" int32_t uniserve_moe_layer_step(const uniserve_moe_layer_call *call, int32_t step, void *stream) {
+  if (call == nullptr) return 1;
   if (step < UNISERVE_MOE_LAYER_ROUTER || step > UNISERVE_MOE_LAYER_UNPERMUTE)
     return ::uniserve::refuse_into(const_cast<char *>(call->error), "moe_layer_step: no step %d", step);
-  return run_layer(call, step, stream);
+  return run_layer(call, step, stream, call->workspace, call->workspace_bytes);
 }

@@ -126,6 +126,7 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
                      : -__builtin_inff();
   }
 
+  UNISERVE_TRACE(20);
   float maximum = values[0];
 #pragma unroll
   for (int it = 0; it < kIter; ++it) maximum = maximum > values[it] ? maximum : values[it];
@@ -149,35 +150,48 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
 #pragma unroll
   for (int it = 0; it < kIter; ++it) values[it] = values[it] / sum;
 
-  // `top` rounds of a (value, lower id) arg-max; lane j keeps round j's pick.
+  UNISERVE_TRACE(21);
+  // `top` rounds of a (value, lower id) arg-max; lane j keeps round j's pick. A round's pick is
+  // the largest probability among the experts not yet taken, the lowest id among equal ones (the
+  // reference's (value, lower id) butterfly, topk_softmax.cu:152-182): the maximum value by a
+  // butterfly of max alone, then the lowest expert holding it by one ballot per slot. A candidate
+  // is a probability (>= 0, never NaN for a finite row) of an expert of the row not yet taken;
+  // the rest stand at -1, below every probability, so a round with no candidate (a row of NaN
+  // scores) names no expert: value -1, expert INT_MAX, as in the reference.
   float picked = 0.0f;
   int picked_expert = 0;
   uint32_t taken = 0u;
+  const uint64_t half_lanes = (lane_id() & kHalf) ? 0xffffffff00000000ull : 0x00000000ffffffffull;
   for (int j = 0; j < top; ++j) {
+    float candidate[kIter];
     float best = -1.0f;
-    int best_expert = INT_MAX;
 #pragma unroll
     for (int it = 0; it < kIter; ++it) {
       const int expert = lane + it * kHalf;
-      if (expert < experts && !((taken >> it) & 1u) && values[it] > best) {
-        best = values[it];
-        best_expert = expert;
+      candidate[it] = (expert < experts && !((taken >> it) & 1u) && values[it] >= 0.0f) ? values[it] : -1.0f;
+      best = best < candidate[it] ? candidate[it] : best;
+    }
+    max_step<16>(best);
+    max_step<8>(best);
+    max_step<4>(best);
+    max_step<2>(best);
+    max_step<1>(best);
+    int best_expert = INT_MAX;
+    if (best >= 0.0f) {
+#pragma unroll
+      for (int it = kIter - 1; it >= 0; --it) {
+        const uint64_t holders = ballot(candidate[it] == best) & half_lanes;
+        if (holders != 0) best_expert = it * kHalf + ((__builtin_ctzll(holders)) & (kHalf - 1));
       }
     }
-    argmax_step<16>(best, best_expert);
-    argmax_step<8>(best, best_expert);
-    argmax_step<4>(best, best_expert);
-    argmax_step<2>(best, best_expert);
-    argmax_step<1>(best, best_expert);
     if (lane == j) {
       picked = best;
       picked_expert = best_expert;
     }
-    // A round that named no expert (a row of NaN scores) marks nothing taken.
-    if (best_expert >= 0 && best_expert < experts && (best_expert & (kHalf - 1)) == lane)
-      taken |= 1u << (best_expert / kHalf);
+    if (best_expert != INT_MAX && (best_expert & (kHalf - 1)) == lane) taken |= 1u << (best_expert / kHalf);
   }
 
+  UNISERVE_TRACE(22);
   float weight = picked;
   if (renormalize) {
     // The butterfly over the next power of two of `top` lanes, lanes past `top` holding zero.

@@ -329,6 +329,7 @@ class LayerViews(ctypes.Structure):
     _fields_ = [
         (name, _I64)
         for name in (
+            "ticket",
             "scores",
             "ids",
             "weights",

@@ -358,7 +358,9 @@ class MoeLayer:
         self.weight_dtype, self.renormalize = weight_dtype, renormalize
         self.device = device or torch.device("cuda")
         self.views = layer_views(max_tokens, hidden_size, experts, top, intermediate, weight_dtype)
-        self.workspace = torch.empty(self.views.total, dtype=torch.uint8, device=self.device)
+        # Zeroed once: the fused front end's counter (the first word) must start at zero, and every
+        # call leaves it zero; nothing else needs initialising.
+        self.workspace = torch.zeros(self.views.total, dtype=torch.uint8, device=self.device)
         self.call = LayerCall()
 
     def view(self, name, dtype, shape):
