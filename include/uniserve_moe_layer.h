@@ -98,6 +98,26 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_views_of(int64_t tokens, int64_t hi
 
 UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_call *call, void *stream);
 
+/// Bytes of the library's per-device scratch for uniserve_moe_layer_no_alloc: the intermediates
+/// of 30B-shaped layers (hidden 2048, intermediate 768, 128 experts, top 8) up to 2991 tokens with
+/// e4m3 weights (3887 bf16; 64 tokens take 90-103 MiB), and of 235B-shaped ones (hidden 4096,
+/// intermediate 1536) up to 543 tokens with e4m3 weights (943 bf16).
+#define UNISERVE_MOE_LAYER_SCRATCH_BYTES (256ll << 20)
+
+/// No counterpart in the reference. For callers that cannot allocate - code under HIP graph
+/// capture, tight serving loops, harnesses that forbid hipMalloc: uniserve_moe_layer with the
+/// intermediates in a library-owned device array of UNISERVE_MOE_LAYER_SCRATCH_BYTES per GPU
+/// (held from the library's load to the process's end) instead of a caller workspace;
+/// `workspace` and `workspace_bytes` are ignored, everything else is read as uniserve_moe_layer
+/// reads it. Extents whose intermediates (uniserve_moe_layer_workspace) exceed the scratch are
+/// refused with a message. Nothing is allocated. The first call on each GPU looks the array's
+/// address up (hipGetSymbolAddress) and clears its counter word on the call's stream: make it
+/// outside stream capture. Every later call finds the counter zero (each call leaves it so) and
+/// needs nothing else cleared: every other intermediate is written before it is read. All calls on
+/// one GPU share its array, so calls that overlap on one GPU (concurrent streams or threads) race;
+/// serialise them.
+UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_layer_call *call, void *stream);
+
 /// The layer's launches in order; the quantiser steps launch nothing for bf16 weights, and
 /// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised. At decode
 /// sizes (at most 4096 routes over at most 512 local experts, a router of at most 1024 experts)

@@ -195,6 +195,9 @@ def test_layer_workspace_and_refusals():
     assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "window" in message(call)
     call.local_offset, call.local_experts, call.activation = 0, 0, 2
     assert lib.uniserve_moe_layer(ctypes.byref(call), None) != 0 and "silu or gelu_tanh" in message(call)
+    # The entry without a workspace refuses extents beyond its scratch before touching a device.
+    call.activation, call.tokens, call.weight_dtype = 0, 8192, abi.DTYPE["f8e4m3"]
+    assert lib.uniserve_moe_layer_no_alloc(ctypes.byref(call), None) != 0 and "scratch" in message(call)
 
 
 def test_sigmoid_gated_add_refusals():

@@ -8,6 +8,7 @@
 // each product are quantised per row per 128 channels first (two more launches); with MXFP4
 // weights they are quantised to MXFP8 (per row per 32 channels, E8M0 scales) the same way.
 #include <cstring>
+#include <mutex>
 
 #include "common.hpp"
 #include "grouped_fp8.hpp"
@@ -499,4 +500,58 @@ extern "C" int32_t uniserve_moe_layer_step(const uniserve_moe_layer_call *call, 
   if (step < UNISERVE_MOE_LAYER_ROUTER || step > UNISERVE_MOE_LAYER_UNPERMUTE)
     return ::uniserve::refuse_into(const_cast<char *>(call->error), "moe_layer_step: no step %d", step);
   return run_layer(call, step, stream, call->workspace, call->workspace_bytes);
+}
+
+// ---- the entry that allocates nothing ------------------------------------------------------------
+
+namespace {
+
+/// The layer's intermediates for callers that pass no workspace: one array per device, held from
+/// the library's load to the process's end. Host code never names it in a launch or a copy: the
+/// name is a host-side stand-in; the device address comes from hipGetSymbolAddress, per device.
+__device__ __align__(256) unsigned char scratch[UNISERVE_MOE_LAYER_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void *scratch_address[kMaxDevices] = {};
+
+/// The device address of `scratch` on the current device, looked up once per device; its first
+/// word (the front end's counter, which every call leaves zero) is cleared on `stream` then.
+hipError_t scratch_of_current_device(void **address, hipStream_t stream) {
+  int device = -1;
+  hipError_t status = hipGetDevice(&device);
+  if (status != hipSuccess) return status;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (scratch_address[device] == nullptr) {
+    void *ptr = nullptr;
+    status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (status != hipSuccess) return status;
+    status = hipMemsetAsync(ptr, 0, uniserve::kFrontTicketBytes, stream);
+    if (status != hipSuccess) return status;
+    scratch_address[device] = ptr;
+  }
+  *address = scratch_address[device];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int32_t uniserve_moe_layer_no_alloc(const uniserve_moe_layer_call *call, void *stream) {
+  using namespace uniserve;
+  return guarded(call, [&]() -> int32_t {
+    uniserve_moe_layer_views v;
+    if (!views_of(call->tokens, call->hidden_size, call->experts, call->top, call->intermediate,
+                  call->weight_dtype, &v))
+      return UNISERVE_REFUSE(call, "moe_layer does not serve these extents or this weight type");
+    if (v.total > UNISERVE_MOE_LAYER_SCRATCH_BYTES)
+      return UNISERVE_REFUSE(call, "moe_layer_no_alloc: these extents need %lld bytes of intermediates, more than "
+                             "the library's %lld-byte scratch; pass a workspace to uniserve_moe_layer instead",
+                             static_cast<long long>(v.total), static_cast<long long>(UNISERVE_MOE_LAYER_SCRATCH_BYTES));
+    void *address = nullptr;
+    const hipError_t status = scratch_of_current_device(&address, static_cast<hipStream_t>(stream));
+    if (status != hipSuccess)
+      return UNISERVE_REFUSE(call, "moe_layer_no_alloc: no scratch address on this device: %s", hipGetErrorString(status));
+    return run_layer(call, -1, stream, address, UNISERVE_MOE_LAYER_SCRATCH_BYTES);
+  });
 }

@@ -395,6 +395,7 @@ _ENTRIES = {
     "uniserve_gather_gemm_fp8_gelu_tanh": GatherFp8Call,
     "uniserve_route_gemm_fp8": RouteFp8Call,
     "uniserve_moe_layer": LayerCall,
+    "uniserve_moe_layer_no_alloc": LayerCall,
     "uniserve_quantize_mxfp8": QuantizeMxfp8Call,
     "uniserve_gather_gemm_mx": GatherMxCall,
     "uniserve_gather_gemm_mx_gelu_tanh": GatherMxCall,
