@@ -89,10 +89,12 @@ __device__ __forceinline__ float silu(float g) {
 
 /// FC1's gate. gelu_tanh(g) = 0.5 g (1 + tanh(u)), u = sqrt(2/pi) (g + 0.044715 g^3), written as
 /// g / (1 + e^(-2u)) (the identity 1 + tanh(u) = 2 / (1 + e^(-2u))), which does not cancel for
-/// large negative g; silu(g) = g / (1 + e^-g). The choice is uniform over a launch.
+/// large negative g; silu(g) = g / (1 + e^-g). The quotient is taken with the hardware reciprocal
+/// (one ulp; the products round the gated values into bf16 next). The choice is uniform over a
+/// launch.
 __device__ __forceinline__ float gate(float g, int32_t activation) {
   const float z = activation == UNISERVE_ACTIVATION_GELU_TANH ? 1.5957691216057308f * (g + 0.044715f * g * g * g) : g;
-  return g / (1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
 }
 
 // ---- MFMA operands ------------------------------------------------------------------------------------

@@ -1,0 +1,426 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The prefill-shaped e4m3 products (FC1 with its gate, or FC2) with 128 x 128 FP32 block scales on
+// gfx950: one workgroup of 8 wavefronts per CU owns one 128-row sort tile and 512 weight rows of
+// its expert (FC1: 256 up rows and the matching 256 gate rows; FC2: 512 output columns).
+//
+// Wavefront w multiplies all 128 tile rows (eight 16-row token blocks) by its own 64 weight rows
+// (four 16-row blocks; FC1: 32 up rows and the 32 gate rows of the same columns), one
+// v_mfma_scale_f32_16x16x128_f8f6f4 per (token block, weight block) and 128-element K stage - one
+// FP32 scale block - whose result is added into the accumulator times s_w * s_x (the weight block's
+// scale, wave-uniform, times the token row's scale of that block).
+//
+// The operands arrive by DMA (`global_load_lds_dwordx4`) and by plain loads issued as inline
+// assembly, all invisible to the compiler, so the loop counts its loads itself and waits with
+// exact vmcnt values:
+//   * each wavefront's weight rows go to a two-stage ring of its own (its rows of stage k are read
+//     into registers at the top of stage k and the buffer is refilled with stage k + 2 right
+//     after): 128 KB of weights, two stages of cover, and no wavefront waits on another's weights;
+//   * the activation rows of the tile (gathered token rows for FC1) go through a two-stage ring
+//     shared by the workgroup, one barrier per stage; that is all 160 KB of the CU's LDS;
+//   * each lane's activation scales (eight token rows per stage, route-major by permuted row)
+//     go to registers, one stage ahead.
+// The MFMAs of a token block go out before the scaling FMAs of the block before it, and the next
+// block's activation fragment is read before they issue, so neither the LDS reads nor the FMAs
+// wait on the MFMAs they follow.
+#pragma once
+
+#include "common.hpp"
+#include "grouped_fp8.hpp"
+#include "grouped_prefill.hpp"
+
+namespace uniserve {
+namespace e4m3 {
+
+constexpr int kRows = 128;                  // tile rows
+constexpr int kWaveRows = 64;               // weight rows per wavefront
+constexpr int kTokenBlocks = kRows / 16;
+constexpr int kWeightLoads = kWaveRows / 8; // 16-byte DMA instructions per wave per stage (8 rows each)
+
+/// One workgroup of 8 wavefronts per CU (512 weight rows), a two-stage weight ring per wavefront
+/// and a two-stage activation ring: all 160 KB of LDS.
+struct Wide {
+  static constexpr int kWaves = 8;
+  static constexpr int kWeightStages = 2;
+  static constexpr int kActStages = 2;
+  static constexpr int kBlocksPerCU = 1;
+};
+/// Two workgroups of 4 wavefronts per CU (256 weight rows each): one stage of weights per
+/// wavefront, refilled as soon as it is read, and a three-stage activation ring - 80 KB each, so
+/// one workgroup's prologue, barriers and epilogue run under the other's MFMAs.
+struct Pair {
+  static constexpr int kWaves = 4;
+  static constexpr int kWeightStages = 1;  // the loop's issue order assumes 1 here when below 2
+  static constexpr int kActStages = 3;
+  static constexpr int kBlocksPerCU = 2;
+};
+
+template <class C>
+struct Shared {
+  u32x4 weights[C::kWeightStages][C::kWaves][kWaveRows * 8];  // each wavefront's own rows
+  u32x4 act[C::kActStages][kRows * 8];                        // chunk c of row r at slot(r, c)
+};
+
+template <class C>
+constexpr int slice_rows() {
+  return C::kWaves * kWaveRows;
+}
+__device__ __forceinline__ int slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+
+/// Lane (r, g)'s e4m3 operand of a 16x16x128 MFMA: K 16 g .. 16 g + 15 and 64 + 16 g .. of `row`.
+__device__ __forceinline__ intx8 fragment(const u32x4 *rows, int row, int g) {
+  const u32x4 lo = rows[slot(row, g)];
+  const u32x4 hi = rows[slot(row, g + 4)];
+  return intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+               static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+}
+
+/// The activation scales of this lane's eight token rows at one K stage: eight 4-byte loads from
+/// `base` + `offset` + 64 tb, issued as inline assembly like the DMA so that the loop's own waits
+/// count them; `wait_scales` is the only place their registers become readable.
+__device__ __forceinline__ void load_scales(float (&out)[kTokenBlocks], const void *base, uint32_t offset) {
+  asm volatile(
+      "global_load_dword %0, %8, %9\n\t"
+      "global_load_dword %1, %8, %9 offset:64\n\t"
+      "global_load_dword %2, %8, %9 offset:128\n\t"
+      "global_load_dword %3, %8, %9 offset:192\n\t"
+      "global_load_dword %4, %8, %9 offset:256\n\t"
+      "global_load_dword %5, %8, %9 offset:320\n\t"
+      "global_load_dword %6, %8, %9 offset:384\n\t"
+      "global_load_dword %7, %8, %9 offset:448\n\t"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]), "=&v"(out[6]),
+        "=&v"(out[7])
+      : "v"(offset), "s"(base));
+}
+constexpr int kScaleLoads = kTokenBlocks;
+
+/// Waits until at most N vector-memory loads of this wave are outstanding (they complete in issue
+/// order), declaring the scale registers written by the wait: the compiler cannot read them, or
+/// move a read of them, before it.
+template <int N>
+__device__ __forceinline__ void wait_loads_and_scales(float (&s)[kTokenBlocks]) {
+  static_assert(N >= 0 && N < 16, "vmcnt's low bits");
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]), "+v"(s[6]), "+v"(s[7])
+               : "n"(N));
+}
+
+/// Bytes of LDS the kernel uses: the operand rings, or the output tile the epilogue stages.
+template <class C, bool kGated>
+constexpr int out_stride() {
+  return (kGated ? slice_rows<C>() / 2 : slice_rows<C>()) * 2 + 8;
+}
+template <class C, bool kGated>
+constexpr int lds_bytes() {
+  return static_cast<int>(sizeof(Shared<C>)) > kRows * out_stride<C, kGated>() ? static_cast<int>(sizeof(Shared<C>))
+                                                                                : kRows * out_stride<C, kGated>();
+}
+
+/// Needs route-major activation scales (p.scale_rows >= the tiles' rows).
+template <class C, bool kGated>
+__global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kernel(PrefillParams p) {
+  using prefill::dma16;
+  using prefill::dma16_after_lds_reads;
+  using prefill::lds_address;
+  constexpr int kWaves = C::kWaves;
+  constexpr int kThreads = kWaves * kWave;
+  constexpr int kSliceRows = slice_rows<C>();
+  constexpr int kActLoads = kRows / 8 / kWaves;  // 16-byte DMA instructions per wave per activation stage
+  static_assert(lds_bytes<C, kGated>() * C::kBlocksPerCU <= 160 * 1024, "the workgroups fit the CU's LDS");
+  __shared__ __align__(16) char lds[lds_bytes<C, kGated>()];
+  Shared<C> &sh = *reinterpret_cast<Shared<C> *>(lds);
+
+  // ---- the work item: groups of `group` tiles, slice-major inside a group, dealt to the XCDs in
+  // turn (block b runs on XCD b % 8) ----
+  const int b = static_cast<int>(blockIdx.x);
+  const int span = p.group * p.slices;
+  const int seq = b >> 3;
+  const int group_index = (seq / span) * 8 + (b & 7);
+  const int first_tile = group_index * p.group;
+  if (first_tile >= p.max_tiles) return;
+  const int in_group = min(p.group, p.max_tiles - first_tile);
+  const int within = seq - (seq / span) * span;
+  if (within >= in_group * p.slices) return;
+  const int slice = within / in_group;
+  const int tile = first_tile + within % in_group;
+  if (tile >= p.num_tiles[0]) return;
+
+  const int64_t expert = p.tile_to_expert[tile];
+  const int64_t first = static_cast<int64_t>(tile) * kRows;
+  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  const int t = static_cast<int>(threadIdx.x);
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int stages = static_cast<int>(p.K / 128);
+  const int top = static_cast<int>(p.top);
+  // The activation row behind tile row r: FC1 gathers token permuted_to_expanded / top (padding
+  // rows read row 0), FC2 reads its own permuted row (padding rows read the tile's first row).
+  auto source_row = [&](int r) -> int64_t {
+    if constexpr (kGated) {
+      const int expanded = p.permuted_to_expanded[first + r];
+      return r < rows ? static_cast<int64_t>(expanded / top) : 0;
+    } else {
+      return r < rows ? first + r : first;
+    }
+  };
+
+  // ---- sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
+  // Activations: wave w brings tile rows kActLoads * 8 w .., instruction i rows
+  // kActLoads * 8 w + 8 i + l / 8, lane l the logical chunk (l % 8) ^ key(row) into physical
+  // chunk l % 8.
+  uint32_t a_off[kActLoads];
+#pragma unroll
+  for (int i = 0; i < kActLoads; ++i) {
+    const int r = kActLoads * 8 * wave + 8 * i + lane / 8;
+    a_off[i] = static_cast<uint32_t>(source_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
+  }
+  // Activation scales ([K / 128, scale_rows] by permuted row): tile row 16 tb + r16 of stage k at
+  // k * scale_rows + first + 16 tb + r16 (padding rows read the scales of rows past the tile's
+  // routes, inside the table, and their products are never stored).
+  const uint32_t sx_off = static_cast<uint32_t>((first + r16) * 4);
+  const int64_t sx_stage = p.scale_rows * 4;
+  // Weights: the wave's 64 rows. FC1 rows 0..31 are up rows slice_col + 32 w .., rows 32..63 the
+  // gate rows of the same columns; FC2 rows are 64 consecutive output columns. Instruction i
+  // fills rows 8 i + l / 8; key(8 i + l / 8) = (l / 16) % 4 + 4 (i % 2).
+  const int64_t slice_col = static_cast<int64_t>(slice) * (kGated ? kSliceRows / 2 : kSliceRows);
+  const int64_t wave_col = slice_col + wave * (kGated ? kWaveRows / 2 : kWaveRows);
+  auto weight_row = [&](int j) -> int64_t {  // weight row of the wave's row j
+    if constexpr (kGated) return j < 32 ? wave_col + j : p.out_width + wave_col + (j - 32);
+    else return wave_col + j;
+  };
+  const uint8_t *w_base[2];
+  w_base[0] = p.weights + (expert * p.n_total + weight_row(0)) * p.K;
+  w_base[1] = p.weights + (expert * p.n_total + weight_row(32)) * p.K;
+  const uint32_t w_lane = static_cast<uint32_t>((lane / 8) * p.K);
+  const uint32_t w_chunk = static_cast<uint32_t>((lane & 7) ^ ((lane >> 4) & 3));
+  // Weight block scales ([experts, n_total / 128, K / 128]): the wave's rows 0..31 and 32..63 each
+  // lie in one 128-row block (FC1: the up and the gate block; FC2: the same block). Lane k holds
+  // stage k's (K / 128 <= 64), read into a scalar per stage.
+  const int64_t blocks_n = p.n_total / 128;
+  const int sw_lane = lane < stages ? lane : 0;
+  const int sw_lanes[2] = {
+      __float_as_int(p.weight_scales[(expert * blocks_n + weight_row(0) / 128) * stages + sw_lane]),
+      __float_as_int(p.weight_scales[(expert * blocks_n + weight_row(32) / 128) * stages + sw_lane])};
+  // Consumed here, so the compiler's wait for these loads comes before the first DMA is issued
+  // (a wait after it would count the DMA too).
+  asm volatile("" ::"v"(sw_lanes[0]), "v"(sw_lanes[1]));
+
+  auto issue_act = [&](int k) {
+    const uint32_t act_lds = lds_address(sh.act[k % C::kActStages] + wave * kActLoads * kWave);
+#pragma unroll
+    for (int i = 0; i < kActLoads; ++i)
+      dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+  };
+  // `after_reads`: the wave just read its rows of the buffer; the first DMA waits for those LDS
+  // reads (lgkmcnt 0) before it may overwrite them.
+  auto issue_weights = [&](int k, bool after_reads) {
+    const uint32_t weight_lds = lds_address(sh.weights[k % C::kWeightStages][wave]);
+#pragma unroll
+    for (int i = 0; i < kWeightLoads; ++i) {
+      const uint8_t *base = w_base[i / 4] + static_cast<int64_t>(k) * 128 + static_cast<int64_t>(i % 4) * 8 * p.K;
+      const uint32_t lane_offset = w_lane + ((w_chunk ^ static_cast<uint32_t>(4 * (i & 1))) << 4);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16);
+      if (i == 0 && after_reads) dma16_after_lds_reads(base, lane_offset, dst);
+      else dma16(base, lane_offset, dst);
+    }
+  };
+  auto issue_scales = [&](float (&out)[kTokenBlocks], int k) {
+    load_scales(out, reinterpret_cast<const uint8_t *>(p.act_scales) + k * sx_stage, sx_off);
+  };
+
+  floatx4 acc[kTokenBlocks][4];
+#pragma unroll
+  for (int tb = 0; tb < kTokenBlocks; ++tb)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) acc[tb][jb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // ---- the K loop. Prefetched during stage k: the activations of stage k + kActStages - 1 (into
+  // the slot stage k - 1 used: every wavefront has passed the barrier after reading it), the
+  // scales of stage k + 1, and - once the wave has read its stage-k weights into registers - its
+  // weights of stage k + kWeightStages. They are issued farthest-ahead last, so that at the top of
+  // stage k + 1 everything but that last group must have landed: the wait, then the barrier for
+  // the other wavefronts' activation rows. Issues past the last stage re-read it (same bytes into
+  // the same places), keeping the counts exact. ----
+  float sx[kTokenBlocks];
+  constexpr bool kWeightsLast = C::kWeightStages > 1;
+  constexpr int kTail = kWeightsLast ? kWeightLoads : (C::kActStages > 2 ? kActLoads : 0);
+  // The prologue issues in the order the loop keeps: the stages needed first, the farthest group last.
+  if constexpr (kWeightsLast) {
+#pragma unroll
+    for (int k = 0; k < C::kActStages - 1; ++k) issue_act(min(k, stages - 1));
+    issue_scales(sx, 0);
+#pragma unroll
+    for (int k = 0; k < C::kWeightStages; ++k) issue_weights(min(k, stages - 1), false);
+  } else {
+#pragma unroll
+    for (int k = 0; k < C::kActStages - 2; ++k) issue_act(min(k, stages - 1));
+    issue_weights(0, false);
+    issue_scales(sx, 0);
+    issue_act(min(C::kActStages - 2, stages - 1));
+  }
+  for (int k = 0; k < stages; ++k) {
+    wait_loads_and_scales<kTail>(sx);
+    __syncthreads();
+    const u32x4 *act = sh.act[k % C::kActStages];
+    const float sw0 = __int_as_float(__builtin_amdgcn_readlane(sw_lanes[0], k));
+    const float sw1 = __int_as_float(__builtin_amdgcn_readlane(sw_lanes[1], k));
+    float sc[kTokenBlocks][2];
+#pragma unroll
+    for (int tb = 0; tb < kTokenBlocks; ++tb) {
+      sc[tb][0] = sx[tb] * sw0;
+      sc[tb][1] = sx[tb] * sw1;
+    }
+    intx8 wf[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) wf[jb] = fragment(sh.weights[k % C::kWeightStages][wave], jb * 16 + r16, g);
+    if constexpr (kWeightsLast) {
+      issue_act(min(k + C::kActStages - 1, stages - 1));
+      issue_scales(sx, min(k + 1, stages - 1));
+      issue_weights(min(k + C::kWeightStages, stages - 1), true);
+    } else {
+      issue_weights(min(k + C::kWeightStages, stages - 1), true);
+      issue_scales(sx, min(k + 1, stages - 1));
+      issue_act(min(k + C::kActStages - 1, stages - 1));
+    }
+
+    intx8 x = fragment(act, r16, g);
+    floatx4 block[2][4];
+#pragma unroll
+    for (int tb = 0; tb <= kTokenBlocks; ++tb) {
+      if (tb < kTokenBlocks) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+          // cbsz/blgp 0: e4m3 x e4m3; scale exponents 127 = 2^0 (the block scales are applied below).
+          block[tb & 1][jb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[jb], x, floatx4{0.0f, 0.0f, 0.0f, 0.0f},
+                                                                              0, 0, 0, 127, 0, 127);
+        if (tb + 1 < kTokenBlocks) x = fragment(act, (tb + 1) * 16 + r16, g);
+      }
+      if (tb > 0) {
+        const int pb = (tb - 1) & 1;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const float s = sc[tb - 1][jb >> 1];
+#ifndef UNISERVE_PROBE_NO_FMA
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[tb - 1][jb][e] = __builtin_fmaf(block[pb][jb][e], s, acc[tb - 1][jb][e]);
+#else
+          acc[tb - 1][jb][0] = __builtin_fmaf(block[pb][jb][0], s, acc[tb - 1][jb][0]);
+#endif
+        }
+      }
+    }
+  }
+  prefill::wait_all_loads();
+  __syncthreads();  // every wave is done with the operand buffers
+#ifdef UNISERVE_PROBE_NO_EPILOGUE
+  if (acc[0][0][0] != 12345.0f) return;
+#endif
+
+  // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row 16 tb + r16
+  // and the wave's weight rows 16 jb + 4 g + e in element e. The output tile goes through LDS so
+  // the global stores are whole rows. ----
+  constexpr int kOutCols = kGated ? kSliceRows / 2 : kSliceRows;
+  constexpr int kOutStride = out_stride<C, kGated>();
+#pragma unroll
+  for (int tb = 0; tb < kTokenBlocks; ++tb) {
+    char *row = lds + (tb * 16 + r16) * kOutStride;
+    if constexpr (kGated) {
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gate(acc[tb][jb + 2][e], p.activation) * acc[tb][jb][e];
+        uint2 packed;
+        packed.x = pack_bf16x2(v[0], v[1]);
+        packed.y = pack_bf16x2(v[2], v[3]);
+        *reinterpret_cast<uint2 *>(row + (wave * 32 + jb * 16 + 4 * g) * 2) = packed;
+      }
+    } else {
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        uint2 packed;
+        packed.x = pack_bf16x2(acc[tb][jb][0], acc[tb][jb][1]);
+        packed.y = pack_bf16x2(acc[tb][jb][2], acc[tb][jb][3]);
+        *reinterpret_cast<uint2 *>(row + (wave * 64 + jb * 16 + 4 * g) * 2) = packed;
+      }
+    }
+  }
+  __syncthreads();
+  if (kGated && p.out_codes != nullptr) {
+    // Written as the FC2 operand: each (row, 128-column group) quantised by 16 lanes from the bf16
+    // values (the stand-alone quantiser's rounding points and encoding: amax of the bf16 values,
+    // s = amax / 448, code = e4m3(v / s)); live rows only.
+    constexpr int kGroups = kOutCols / 128;
+    const int sub = t & 15;
+    const int64_t groups_per_row = p.out_width / 128;
+    for (int index = t / 16; index < kRows * kGroups; index += kThreads / 16) {
+      const int m = index / kGroups;
+      const int group = index - m * kGroups;
+      const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + (group * 128 + sub * 8) * 2);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(piece[j] << 16);
+        v[2 * j + 1] = __uint_as_float(piece[j] & 0xffff0000u);
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+#pragma unroll
+      for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+      if (m >= rows) continue;
+      const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+      const int64_t column = slice_col + group * 128 + sub * 8;
+      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(v, scale);
+      if (sub == 0) {
+        const int64_t at = p.scale_rows != 0 ? column / 128 * p.scale_rows + first + m
+                                             : (first + m) * groups_per_row + column / 128;
+        p.out_code_scales[at] = scale;
+      }
+    }
+    return;
+  }
+  constexpr int kPieces = kOutCols / 8;
+  for (int index = t; index < kRows * kPieces; index += kThreads) {
+    const int m = index / kPieces;
+    const int c = index - m * kPieces;
+    if (m >= rows) continue;
+    const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + c * 16);
+    *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
+  }
+}
+
+}  // namespace e4m3
+
+/// Whether the e4m3 kernel serves the shape: whole 128-K stages (at most 64 of them), whole slices
+/// (FC1 128 output columns, FC2 256) and route-major activation scales.
+inline bool e4m3_fits(bool gated, int64_t K, int64_t out_width, int64_t scale_rows) {
+  const int64_t columns = gated ? e4m3::slice_rows<e4m3::Pair>() / 2 : e4m3::slice_rows<e4m3::Pair>();
+  return K % 128 == 0 && K > 0 && K / 128 <= kWave && out_width % columns == 0 && scale_rows != 0;
+}
+
+/// Launches it over `max_tiles` tiles (tiles past `num_tiles` exit at once); with `p.out_codes`
+/// set (FC1 only) the gated rows are written as e4m3 codes and scales.
+#ifndef UNISERVE_E4M3_GROUP
+#define UNISERVE_E4M3_GROUP 4
+#endif
+#ifndef UNISERVE_E4M3_CONFIG
+#define UNISERVE_E4M3_CONFIG Pair
+#endif
+inline void launch_e4m3(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream,
+                        int group = UNISERVE_E4M3_GROUP) {
+  using C = e4m3::UNISERVE_E4M3_CONFIG;
+  const int64_t columns = gated ? e4m3::slice_rows<C>() / 2 : e4m3::slice_rows<C>();
+  p.slices = static_cast<int32_t>(p.out_width / columns);
+  p.max_tiles = static_cast<int32_t>(max_tiles);
+  p.group = group;
+  p.groups_per_xcd = static_cast<int32_t>(ceil_div<int64_t>(ceil_div<int64_t>(max_tiles, group), 8));
+  const dim3 grid(static_cast<uint32_t>(static_cast<int64_t>(p.groups_per_xcd) * group * p.slices * 8));
+  const dim3 block(static_cast<uint32_t>(C::kWaves * kWave));
+  if (gated) hipLaunchKernelGGL((e4m3::e4m3_kernel<C, true>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((e4m3::e4m3_kernel<C, false>), grid, block, 0, stream, p);
+}
+
+}  // namespace uniserve

@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_dual.hpp"
+#include "grouped_e4m3.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_moe_fp8.h"
 
@@ -514,9 +515,9 @@ void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scal
 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream) {
-  // The two-workgroup kernel first, then the 8-wave one (whole 256-K stage pairs), then the
-  // generic tiled kernel.
-  const bool fits = dual_fits(gated, p.K, p.out_width, p.out_codes != nullptr) ||
+  // The 8-wave kernel with per-wave weight buffers first, then the two-workgroup kernel, then the
+  // 8-wave kernel of whole 256-K stage pairs, then the generic tiled kernel.
+  const bool fits = e4m3_fits(gated, p.K, p.out_width, p.scale_rows) || dual_fits(gated, p.K, p.out_width, p.out_codes != nullptr) ||
                     (gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
                            : prefill_fits<prefill::E4m3, false>(p.K, p.out_width));
   if (!stream_path && fits) {
@@ -538,6 +539,12 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
     q.scale_rows = p.scale_rows;
+#ifndef UNISERVE_FP8_PREFILL_DUAL
+    if (e4m3_fits(gated, q.K, q.out_width, q.scale_rows)) {
+      launch_e4m3(q, gated, max_tiles, stream);
+      return;
+    }
+#endif
     if (dual_fits(gated, q.K, q.out_width, q.out_codes != nullptr)) {
       launch_dual_e4m3(q, gated, max_tiles, stream);
       return;
@@ -596,7 +603,8 @@ namespace uniserve {
 
 bool fp8_fc1_quantizes(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate) {
   return !fp8_stream_path(tokens * top, experts) &&
-         (dual_fits(true, hidden_size, intermediate, true) || prefill_fits<prefill::E4m3, true>(hidden_size, intermediate));
+         (dual_fits(true, hidden_size, intermediate, true) ||
+          prefill_fits<prefill::E4m3, true>(hidden_size, intermediate));
 }
 
 bool fp8_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidden_size, int64_t intermediate,
