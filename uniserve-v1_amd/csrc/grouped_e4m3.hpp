@@ -75,9 +75,20 @@ __device__ __forceinline__ intx8 fragment(const u32x4 *rows, int row, int g) {
                static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
 }
 
+/// One 4-byte DMA per lane from `base` + `offset` into LDS at `lds` + 4 * lane.
+__device__ __forceinline__ void dma4(const void *base, uint32_t offset, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %0, %1\n\t"
+      :
+      : "v"(offset), "s"(base), "s"(lds)
+      : "m0");
+}
+
 /// The activation scales of this lane's eight token rows at one K stage: eight 4-byte loads from
 /// `base` + `offset` + 64 tb, issued as inline assembly like the DMA so that the loop's own waits
-/// count them; `wait_scales` is the only place their registers become readable.
+/// count them; `wait_loads_and_scales` is the only place their registers become readable.
 __device__ __forceinline__ void load_scales(float (&out)[kTokenBlocks], const void *base, uint32_t offset) {
   asm volatile(
       "global_load_dword %0, %8, %9\n\t"
@@ -96,7 +107,8 @@ constexpr int kScaleLoads = kTokenBlocks;
 
 /// Waits until at most N vector-memory loads of this wave are outstanding (they complete in issue
 /// order), declaring the scale registers written by the wait: the compiler cannot read them, or
-/// move a read of them, before it.
+/// move a read of them, before it. The loads and this wait sit in one straight stretch of a loop
+/// iteration, so no control-flow merge makes the compiler copy the registers in between.
 template <int N>
 __device__ __forceinline__ void wait_loads_and_scales(float (&s)[kTokenBlocks]) {
   static_assert(N >= 0 && N < 16, "vmcnt's low bits");
@@ -229,6 +241,24 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
   auto issue_scales = [&](float (&out)[kTokenBlocks], int k) {
     load_scales(out, reinterpret_cast<const uint8_t *>(p.act_scales) + k * sx_stage, sx_off);
   };
+  // Past the last stage the loop issues the same number of loads, each 4 bytes per lane from the
+  // scale table the loop just read (cache-resident), into LDS nobody reads any more, so that every
+  // wait counts alike without re-reading whole stages.
+  const uint8_t *dummy_source = reinterpret_cast<const uint8_t *>(p.act_scales);
+  auto issue_act_dummy = [&](int k) {
+    const uint32_t act_lds = lds_address(sh.act[k % C::kActStages] + wave * kActLoads * kWave);
+#pragma unroll
+    for (int i = 0; i < kActLoads; ++i)
+      e4m3::dma4(dummy_source, sx_off, __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+  };
+  auto issue_weights_dummy = [&](int k) {
+    const uint32_t weight_lds = lds_address(sh.weights[k % C::kWeightStages][wave]);
+#pragma unroll
+    for (int i = 0; i < kWeightLoads; ++i) {
+      if (i == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      e4m3::dma4(dummy_source, sx_off, __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
+    }
+  };
 
   floatx4 acc[kTokenBlocks][4];
 #pragma unroll
@@ -239,29 +269,32 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
   // ---- the K loop. Prefetched during stage k: the activations of stage k + kActStages - 1 (into
   // the slot stage k - 1 used: every wavefront has passed the barrier after reading it), the
   // scales of stage k + 1, and - once the wave has read its stage-k weights into registers - its
-  // weights of stage k + kWeightStages. They are issued farthest-ahead last, so that at the top of
-  // stage k + 1 everything but that last group must have landed: the wait, then the barrier for
-  // the other wavefronts' activation rows. Issues past the last stage re-read it (same bytes into
-  // the same places), keeping the counts exact. ----
-  float sx[kTokenBlocks];
+  // weights of stage k + kWeightStages (stand-in loads past the last stage). They are issued
+  // farthest-ahead last: at the end of stage k everything up to the scales of stage k + 1 has
+  // landed (the wait that makes the scale registers readable), at the top of stage k + 1
+  // everything but the farthest group, then the barrier for the other wavefronts' activation
+  // rows. ----
   constexpr bool kWeightsLast = C::kWeightStages > 1;
-  constexpr int kTail = kWeightsLast ? kWeightLoads : (C::kActStages > 2 ? kActLoads : 0);
-  // The prologue issues in the order the loop keeps: the stages needed first, the farthest group last.
+  constexpr int kLast = kWeightsLast ? kWeightLoads : kActLoads;  // loads of the farthest group
+  float sx[kTokenBlocks];
+  // (At least kActStages and kWeightStages stages: e4m3_fits.)
   if constexpr (kWeightsLast) {
 #pragma unroll
-    for (int k = 0; k < C::kActStages - 1; ++k) issue_act(min(k, stages - 1));
+    for (int k = 0; k < C::kActStages - 1; ++k) issue_act(k);
     issue_scales(sx, 0);
 #pragma unroll
-    for (int k = 0; k < C::kWeightStages; ++k) issue_weights(min(k, stages - 1), false);
+    for (int k = 0; k < C::kWeightStages; ++k) issue_weights(k, false);
   } else {
+    static_assert(C::kWeightStages == 1 && C::kActStages >= 2, "the issue orders written here");
 #pragma unroll
-    for (int k = 0; k < C::kActStages - 2; ++k) issue_act(min(k, stages - 1));
+    for (int k = 0; k < C::kActStages - 2; ++k) issue_act(k);
     issue_weights(0, false);
     issue_scales(sx, 0);
-    issue_act(min(C::kActStages - 2, stages - 1));
+    issue_act(C::kActStages - 2);
   }
+  wait_loads_and_scales<kLast>(sx);
   for (int k = 0; k < stages; ++k) {
-    wait_loads_and_scales<kTail>(sx);
+    prefill::wait_loads_but<kLast>();
     __syncthreads();
     const u32x4 *act = sh.act[k % C::kActStages];
     const float sw0 = __int_as_float(__builtin_amdgcn_readlane(sw_lanes[0], k));
@@ -275,47 +308,78 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
     intx8 wf[4];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) wf[jb] = fragment(sh.weights[k % C::kWeightStages][wave], jb * 16 + r16, g);
+    const int act_next = k + C::kActStages - 1;
+    const int weights_next = k + C::kWeightStages;
+    auto act_group = [&] {
+      if (act_next < stages) issue_act(act_next);
+      else issue_act_dummy(act_next);
+    };
+    auto weight_group = [&] {
+      if (weights_next < stages) issue_weights(weights_next, true);
+      else issue_weights_dummy(weights_next);
+    };
     if constexpr (kWeightsLast) {
-      issue_act(min(k + C::kActStages - 1, stages - 1));
+      act_group();
       issue_scales(sx, min(k + 1, stages - 1));
-      issue_weights(min(k + C::kWeightStages, stages - 1), true);
+      weight_group();
     } else {
-      issue_weights(min(k + C::kWeightStages, stages - 1), true);
+      weight_group();
       issue_scales(sx, min(k + 1, stages - 1));
-      issue_act(min(k + C::kActStages - 1, stages - 1));
+      act_group();
     }
+#ifdef UNISERVE_PROBE_NO_LOOP
+    if (k >= 0) break;
+#endif
 
-    intx8 x = fragment(act, r16, g);
-    floatx4 block[2][4];
-#pragma unroll
-    for (int tb = 0; tb <= kTokenBlocks; ++tb) {
-      if (tb < kTokenBlocks) {
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-          // cbsz/blgp 0: e4m3 x e4m3; scale exponents 127 = 2^0 (the block scales are applied below).
-          block[tb & 1][jb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[jb], x, floatx4{0.0f, 0.0f, 0.0f, 0.0f},
-                                                                              0, 0, 0, 127, 0, 127);
-        if (tb + 1 < kTokenBlocks) x = fragment(act, (tb + 1) * 16 + r16, g);
-      }
-      if (tb > 0) {
-        const int pb = (tb - 1) & 1;
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          const float s = sc[tb - 1][jb >> 1];
+    // Per token block: the MFMAs of weight blocks 0 and 1, the scaling of the previous token
+    // block's blocks 2 and 3, the MFMAs of blocks 2 and 3, the scaling of this block's 0 and 1 -
+    // each scaling two MFMAs behind the results it reads, and four block results live at most.
+    auto scale_into = [&](floatx4 &into, const floatx4 &result, float s) {
 #ifndef UNISERVE_PROBE_NO_FMA
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[tb - 1][jb][e] = __builtin_fmaf(block[pb][jb][e], s, acc[tb - 1][jb][e]);
+      for (int e = 0; e < 4; ++e) into[e] = __builtin_fmaf(result[e], s, into[e]);
 #else
-          acc[tb - 1][jb][0] = __builtin_fmaf(block[pb][jb][0], s, acc[tb - 1][jb][0]);
+      into[0] = __builtin_fmaf(result[0], s, into[0]);
 #endif
-        }
+    };
+    // cbsz/blgp 0: e4m3 x e4m3; scale exponents 127 = 2^0 (the block scales are applied after).
+    auto mfma = [&](const intx8 &w, const intx8 &a) {
+      return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, a, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
+    };
+    intx8 x = fragment(act, r16, g);
+    floatx4 lower[2], upper[2];
+#pragma unroll
+    for (int tb = 0; tb < kTokenBlocks; ++tb) {
+      lower[0] = mfma(wf[0], x);
+      lower[1] = mfma(wf[1], x);
+      if (tb > 0) {
+        scale_into(acc[tb - 1][2], upper[0], sc[tb - 1][1]);
+        scale_into(acc[tb - 1][3], upper[1], sc[tb - 1][1]);
       }
+      upper[0] = mfma(wf[2], x);
+      upper[1] = mfma(wf[3], x);
+      if (tb + 1 < kTokenBlocks) x = fragment(act, (tb + 1) * 16 + r16, g);
+      scale_into(acc[tb][0], lower[0], sc[tb][0]);
+      scale_into(acc[tb][1], lower[1], sc[tb][0]);
     }
+    scale_into(acc[kTokenBlocks - 1][2], upper[0], sc[kTokenBlocks - 1][1]);
+    scale_into(acc[kTokenBlocks - 1][3], upper[1], sc[kTokenBlocks - 1][1]);
+    wait_loads_and_scales<kLast>(sx);
   }
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done with the operand buffers
 #ifdef UNISERVE_PROBE_NO_EPILOGUE
-  if (acc[0][0][0] != 12345.0f) return;
+  {
+    float keep = 0.0f;
+#pragma unroll
+    for (int tb = 0; tb < kTokenBlocks; ++tb)
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) keep += acc[tb][jb][e];
+    if (keep == 12345.0f) p.out[t] = 1;
+    return;
+  }
 #endif
 
   // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row 16 tb + r16
@@ -394,11 +458,11 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
 
 }  // namespace e4m3
 
-/// Whether the e4m3 kernel serves the shape: whole 128-K stages (at most 64 of them), whole slices
+/// Whether the e4m3 kernel serves the shape: whole 128-K stages (3 to 64 of them), whole slices
 /// (FC1 128 output columns, FC2 256) and route-major activation scales.
 inline bool e4m3_fits(bool gated, int64_t K, int64_t out_width, int64_t scale_rows) {
   const int64_t columns = gated ? e4m3::slice_rows<e4m3::Pair>() / 2 : e4m3::slice_rows<e4m3::Pair>();
-  return K % 128 == 0 && K > 0 && K / 128 <= kWave && out_width % columns == 0 && scale_rows != 0;
+  return K % 128 == 0 && K / 128 >= 3 && K / 128 <= kWave && out_width % columns == 0 && scale_rows != 0;
 }
 
 /// Launches it over `max_tiles` tiles (tiles past `num_tiles` exit at once); with `p.out_codes`
