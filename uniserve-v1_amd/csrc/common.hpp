@@ -10,6 +10,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <exception>
+#include <type_traits>
 
 #include "uniserve_abi.h"
 
@@ -78,8 +79,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float value) {
   return static_cast<uint16_t>(bits >> 16);
 }
 
+/// Two values rounded as f32_to_bf16 does, packed low to high, by gfx950's v_cvt_pk_bf16_f32
+/// (identical to f32_to_bf16 on every float, NaNs included - checked exhaustively on the device).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  typedef float floatx2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2{lo, hi}), bf16x2));
 }
 
 /// silu(g) = g / (1 + e^-g), with the hardware exponential (v_exp_f32 on g * -log2 e).
@@ -92,6 +97,12 @@ __device__ __forceinline__ float silu(float g) {
 /// large negative g; silu(g) = g / (1 + e^-g). The quotient is taken with the hardware reciprocal
 /// (one ulp; the products round the gated values into bf16 next). The choice is uniform over a
 /// launch.
+template <int kActivation>
+__device__ __forceinline__ float gate_of(float g) {
+  const float z = kActivation == UNISERVE_ACTIVATION_GELU_TANH ? 1.5957691216057308f * (g + 0.044715f * g * g * g) : g;
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
+}
+/// The same with the activation chosen at run time.
 __device__ __forceinline__ float gate(float g, int32_t activation) {
   const float z = activation == UNISERVE_ACTIVATION_GELU_TANH ? 1.5957691216057308f * (g + 0.044715f * g * g * g) : g;
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
@@ -118,6 +129,17 @@ __device__ __forceinline__ floatx4 mfma_16x16x128_fp8(intx8 a, intx8 b, floatx4 
 }
 
 // ---- wave64 helpers --------------------------------------------------------------------------------------
+
+/// The maximum over each 16-lane row of the wavefront, in every lane of the row, by DPP moves:
+/// quad_perm [1,0,3,2] and [2,3,0,1] (the quad), row_half_mirror (the other quad of the
+/// eight), row_mirror (the other eight); NaNs drop out as in fmaxf.
+__device__ __forceinline__ float row16_max(float x) {
+  x = __builtin_fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xb1, 0xf, 0xf, false)));
+  x = __builtin_fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4e, 0xf, 0xf, false)));
+  x = __builtin_fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false)));
+  x = __builtin_fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false)));
+  return x;
+}
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & (kWave - 1)); }
 

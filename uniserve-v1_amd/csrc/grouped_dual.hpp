@@ -323,11 +323,10 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
       float amax = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
-#pragma unroll
-      for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+      amax = row16_max(amax);
       if (m >= rows) continue;
       const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + slice_col + sub * 8) = e4m3_eight(v, scale);
+      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + slice_col + sub * 8) = e4m3_eight_of_bf16(v, scale);
       if (sub == 0) {
         const int64_t at = p.scale_rows != 0 ? slice_col / 128 * p.scale_rows + first + m
                                              : (first + m) * groups_per_row + slice_col / 128;

@@ -29,6 +29,30 @@
 #include "grouped_fp8.hpp"
 #include "grouped_prefill.hpp"
 
+#ifdef UNISERVE_E4M3_TRACE
+// Timing of each workgroup (start, loop end, end in s_memrealtime ticks; HW_ID; XCC_ID), read back
+// by uniserve_e4m3_trace_read in builds made with this macro only.
+__device__ unsigned long long e4m3_trace[16384][8];
+#define UNISERVE_E4M3_MARK(slot)                                                                        \
+  do {                                                                                                  \
+    if (threadIdx.x == 0 && blockIdx.x < 16384) e4m3_trace[blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#ifdef UNISERVE_E4M3_LOOPTRACE
+#define UNISERVE_E4M3_EPI_MARK(slot) \
+  do {                               \
+  } while (0)
+#else
+#define UNISERVE_E4M3_EPI_MARK(slot) UNISERVE_E4M3_MARK(slot)
+#endif
+#else
+#define UNISERVE_E4M3_EPI_MARK(slot) \
+  do {                               \
+  } while (0)
+#define UNISERVE_E4M3_MARK(slot) \
+  do {                           \
+  } while (0)
+#endif
+
 namespace uniserve {
 namespace e4m3 {
 
@@ -37,14 +61,6 @@ constexpr int kWaveRows = 64;               // weight rows per wavefront
 constexpr int kTokenBlocks = kRows / 16;
 constexpr int kWeightLoads = kWaveRows / 8; // 16-byte DMA instructions per wave per stage (8 rows each)
 
-/// One workgroup of 8 wavefronts per CU (512 weight rows), a two-stage weight ring per wavefront
-/// and a two-stage activation ring: all 160 KB of LDS.
-struct Wide {
-  static constexpr int kWaves = 8;
-  static constexpr int kWeightStages = 2;
-  static constexpr int kActStages = 2;
-  static constexpr int kBlocksPerCU = 1;
-};
 /// Two workgroups of 4 wavefronts per CU (256 weight rows each): one stage of weights per
 /// wavefront, refilled as soon as it is read, and a three-stage activation ring - 80 KB each, so
 /// one workgroup's prologue, barriers and epilogue run under the other's MFMAs.
@@ -103,6 +119,17 @@ __device__ __forceinline__ void load_scales(float (&out)[kTokenBlocks], const vo
         "=&v"(out[7])
       : "v"(offset), "s"(base));
 }
+/// Half of load_scales: token blocks 4 h .. 4 h + 3.
+template <int kHalf>
+__device__ __forceinline__ void load_scales_half(float (&out)[kTokenBlocks], const void *base, uint32_t offset) {
+  asm volatile(
+      "global_load_dword %0, %4, %5 offset:%6\n\t"
+      "global_load_dword %1, %4, %5 offset:%7\n\t"
+      "global_load_dword %2, %4, %5 offset:%8\n\t"
+      "global_load_dword %3, %4, %5 offset:%9\n\t"
+      : "=&v"(out[4 * kHalf]), "=&v"(out[4 * kHalf + 1]), "=&v"(out[4 * kHalf + 2]), "=&v"(out[4 * kHalf + 3])
+      : "v"(offset), "s"(base), "n"(256 * kHalf), "n"(256 * kHalf + 64), "n"(256 * kHalf + 128), "n"(256 * kHalf + 192));
+}
 constexpr int kScaleLoads = kTokenBlocks;
 
 /// Waits until at most N vector-memory loads of this wave are outstanding (they complete in issue
@@ -157,6 +184,12 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
   const int tile = first_tile + within % in_group;
   if (tile >= p.num_tiles[0]) return;
 
+  UNISERVE_E4M3_MARK(0);
+#ifdef UNISERVE_E4M3_TRACE
+  if (threadIdx.x == 0)
+    e4m3_trace[blockIdx.x][3] = (static_cast<unsigned long long>(__builtin_amdgcn_s_getreg((31 << 11) | 20)) << 32) |
+                                __builtin_amdgcn_s_getreg((31 << 11) | 4);
+#endif
   const int64_t expert = p.tile_to_expert[tile];
   const int64_t first = static_cast<int64_t>(tile) * kRows;
   const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
@@ -241,24 +274,28 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
   auto issue_scales = [&](float (&out)[kTokenBlocks], int k) {
     load_scales(out, reinterpret_cast<const uint8_t *>(p.act_scales) + k * sx_stage, sx_off);
   };
-  // Past the last stage the loop issues the same number of loads, each 4 bytes per lane from the
-  // scale table the loop just read (cache-resident), into LDS nobody reads any more, so that every
-  // wait counts alike without re-reading whole stages.
-  const uint8_t *dummy_source = reinterpret_cast<const uint8_t *>(p.act_scales);
-  auto issue_act_dummy = [&](int k) {
-    const uint32_t act_lds = lds_address(sh.act[k % C::kActStages] + wave * kActLoads * kWave);
+  // Halves of the groups above, issued in the loop between MFMAs.
+  auto issue_weights_part = [&](int k, int half) {
+    const uint32_t weight_lds = lds_address(sh.weights[0][wave]);
 #pragma unroll
-    for (int i = 0; i < kActLoads; ++i)
-      e4m3::dma4(dummy_source, sx_off, __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
-  };
-  auto issue_weights_dummy = [&](int k) {
-    const uint32_t weight_lds = lds_address(sh.weights[k % C::kWeightStages][wave]);
-#pragma unroll
-    for (int i = 0; i < kWeightLoads; ++i) {
-      if (i == 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      e4m3::dma4(dummy_source, sx_off, __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16));
+    for (int j = 0; j < kWeightLoads / 2; ++j) {
+      const int i = half * (kWeightLoads / 2) + j;
+      const uint8_t *base = w_base[i / 4] + static_cast<int64_t>(k) * 128 + static_cast<int64_t>(i % 4) * 8 * p.K;
+      const uint32_t lane_offset = w_lane + ((w_chunk ^ static_cast<uint32_t>(4 * (i & 1))) << 4);
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16);
+      if (i == 0) dma16_after_lds_reads(base, lane_offset, dst);
+      else dma16(base, lane_offset, dst);
     }
   };
+  auto issue_act_part = [&](int k, int half) {
+    const uint32_t act_lds = lds_address(sh.act[k % C::kActStages] + wave * kActLoads * kWave);
+#pragma unroll
+    for (int j = 0; j < kActLoads / 2; ++j) {
+      const int i = half * (kActLoads / 2) + j;
+      dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+    }
+  };
+  const uint8_t *scale_table = reinterpret_cast<const uint8_t *>(p.act_scales);
 
   floatx4 acc[kTokenBlocks][4];
 #pragma unroll
@@ -268,34 +305,42 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
 
   // ---- the K loop. Prefetched during stage k: the activations of stage k + kActStages - 1 (into
   // the slot stage k - 1 used: every wavefront has passed the barrier after reading it), the
-  // scales of stage k + 1, and - once the wave has read its stage-k weights into registers - its
-  // weights of stage k + kWeightStages (stand-in loads past the last stage). They are issued
-  // farthest-ahead last: at the end of stage k everything up to the scales of stage k + 1 has
-  // landed (the wait that makes the scale registers readable), at the top of stage k + 1
-  // everything but the farthest group, then the barrier for the other wavefronts' activation
-  // rows. ----
-  constexpr bool kWeightsLast = C::kWeightStages > 1;
-  constexpr int kLast = kWeightsLast ? kWeightLoads : kActLoads;  // loads of the farthest group
+  // scales of stage k + 1 and - the wave has read its stage-k weights into registers at the top -
+  // its weights of stage k + 1; past the last stage, the last stage again (cache-resident, into
+  // buffers nobody reads), so that every wait counts alike. They go out in that order - weights,
+  // scales, activations - spread over the first token blocks' MFMAs, so that no wave stalls long
+  // on a full memory queue with its MFMAs unissued. At the end of stage k everything up to the
+  // scales of stage k + 1 has landed (the wait that makes the scale registers readable), at the
+  // top of stage k + 1 everything but the activations, then the barrier for the other
+  // wavefronts' activation rows. ----
+  static_assert(C::kWeightStages == 1 && C::kActStages >= 2, "the issue orders written here");
+  constexpr int kLast = kActLoads;  // loads of the farthest group
   float sx[kTokenBlocks];
-  // (At least kActStages and kWeightStages stages: e4m3_fits.)
-  if constexpr (kWeightsLast) {
+  // (At least kActStages stages: e4m3_fits.)
 #pragma unroll
-    for (int k = 0; k < C::kActStages - 1; ++k) issue_act(k);
-    issue_scales(sx, 0);
-#pragma unroll
-    for (int k = 0; k < C::kWeightStages; ++k) issue_weights(k, false);
-  } else {
-    static_assert(C::kWeightStages == 1 && C::kActStages >= 2, "the issue orders written here");
-#pragma unroll
-    for (int k = 0; k < C::kActStages - 2; ++k) issue_act(k);
-    issue_weights(0, false);
-    issue_scales(sx, 0);
-    issue_act(C::kActStages - 2);
-  }
+  for (int k = 0; k < C::kActStages - 2; ++k) issue_act(k);
+  issue_weights(0, false);
+  issue_scales(sx, 0);
+  issue_act(C::kActStages - 2);
   wait_loads_and_scales<kLast>(sx);
+  UNISERVE_E4M3_MARK(7);
+#ifdef UNISERVE_E4M3_LOOPTRACE
+  unsigned long long spent_top = 0, spent_barrier = 0, spent_end = 0;
+  const unsigned long long loop_start = __builtin_amdgcn_s_memtime();
+#endif
   for (int k = 0; k < stages; ++k) {
+#ifdef UNISERVE_E4M3_LOOPTRACE
+    const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+    prefill::wait_loads_but<kLast>();
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+    __syncthreads();
+    const unsigned long long c2 = __builtin_amdgcn_s_memtime();
+    spent_top += c1 - c0;
+    spent_barrier += c2 - c1;
+#else
     prefill::wait_loads_but<kLast>();
     __syncthreads();
+#endif
     const u32x4 *act = sh.act[k % C::kActStages];
     const float sw0 = __int_as_float(__builtin_amdgcn_readlane(sw_lanes[0], k));
     const float sw1 = __int_as_float(__builtin_amdgcn_readlane(sw_lanes[1], k));
@@ -307,26 +352,20 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
     }
     intx8 wf[4];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) wf[jb] = fragment(sh.weights[k % C::kWeightStages][wave], jb * 16 + r16, g);
-    const int act_next = k + C::kActStages - 1;
-    const int weights_next = k + C::kWeightStages;
-    auto act_group = [&] {
-      if (act_next < stages) issue_act(act_next);
-      else issue_act_dummy(act_next);
+    for (int jb = 0; jb < 4; ++jb) wf[jb] = fragment(sh.weights[0][wave], jb * 16 + r16, g);
+    const int act_next = min(k + C::kActStages - 1, stages - 1);
+    const int next = min(k + 1, stages - 1);
+    // The loads issued before token block tb's MFMAs.
+    auto issue_part = [&](int tb) {
+#ifndef UNISERVE_PROBE_NO_LOADS
+      if (tb == 0) issue_weights_part(next, 0);
+      if (tb == 1) issue_weights_part(next, 1);
+      if (tb == 2) load_scales_half<0>(sx, scale_table + next * sx_stage, sx_off);
+      if (tb == 3) load_scales_half<1>(sx, scale_table + next * sx_stage, sx_off);
+      if (tb == 4) issue_act_part(act_next, 0);
+      if (tb == 5) issue_act_part(act_next, 1);
+#endif
     };
-    auto weight_group = [&] {
-      if (weights_next < stages) issue_weights(weights_next, true);
-      else issue_weights_dummy(weights_next);
-    };
-    if constexpr (kWeightsLast) {
-      act_group();
-      issue_scales(sx, min(k + 1, stages - 1));
-      weight_group();
-    } else {
-      weight_group();
-      issue_scales(sx, min(k + 1, stages - 1));
-      act_group();
-    }
 #ifdef UNISERVE_PROBE_NO_LOOP
     if (k >= 0) break;
 #endif
@@ -346,10 +385,35 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
     auto mfma = [&](const intx8 &w, const intx8 &a) {
       return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, a, floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, 127, 0, 127);
     };
+#ifndef UNISERVE_E4M3_OLD_ORDER
+    // The stage's 32 MFMAs in (token block, weight block) order; after issuing MFMA n the wave
+    // scales the result of MFMA n - 2 (done by then: the matrix pipe runs one MFMA at a time),
+    // and the next token block's activation fragment is read three MFMAs before its first use.
+    intx8 x = fragment(act, r16, g), x_next;
+    floatx4 result[3];
+#pragma unroll
+    for (int n = 0; n < kTokenBlocks * 4; ++n) {
+      const int tb = n / 4, jb = n % 4;
+      if (jb == 0) issue_part(tb);
+      result[n % 3] = mfma(wf[jb], x);
+      if (jb == 0 && tb + 1 < kTokenBlocks) x_next = fragment(act, (tb + 1) * 16 + r16, g);
+      if (n >= 2) {
+        const int m = n - 2;
+        scale_into(acc[m / 4][m % 4], result[m % 3], sc[m / 4][(m % 4) / 2]);
+      }
+      if (jb == 3 && tb + 1 < kTokenBlocks) x = x_next;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // the MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then four VALU (the scaling)
+    }
+#pragma unroll
+    for (int m = kTokenBlocks * 4 - 2; m < kTokenBlocks * 4; ++m)
+      scale_into(acc[m / 4][m % 4], result[m % 3], sc[m / 4][(m % 4) / 2]);
+#else
     intx8 x = fragment(act, r16, g);
     floatx4 lower[2], upper[2];
 #pragma unroll
     for (int tb = 0; tb < kTokenBlocks; ++tb) {
+      issue_part(tb);
       lower[0] = mfma(wf[0], x);
       lower[1] = mfma(wf[1], x);
       if (tb > 0) {
@@ -364,10 +428,26 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
     }
     scale_into(acc[kTokenBlocks - 1][2], upper[0], sc[kTokenBlocks - 1][1]);
     scale_into(acc[kTokenBlocks - 1][3], upper[1], sc[kTokenBlocks - 1][1]);
+#endif
+#ifdef UNISERVE_E4M3_LOOPTRACE
+    const unsigned long long c3 = __builtin_amdgcn_s_memtime();
     wait_loads_and_scales<kLast>(sx);
+    spent_end += __builtin_amdgcn_s_memtime() - c3;
+#else
+    wait_loads_and_scales<kLast>(sx);
+#endif
   }
+#ifdef UNISERVE_E4M3_LOOPTRACE
+  if (threadIdx.x == 0 && blockIdx.x < 16384) {
+    e4m3_trace[blockIdx.x][4] = spent_top;
+    e4m3_trace[blockIdx.x][5] = spent_barrier;
+    e4m3_trace[blockIdx.x][6] = spent_end;
+    e4m3_trace[blockIdx.x][2] = __builtin_amdgcn_s_memtime() - loop_start;
+  }
+#endif
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done with the operand buffers
+  UNISERVE_E4M3_MARK(1);
 #ifdef UNISERVE_PROBE_NO_EPILOGUE
   {
     float keep = 0.0f;
@@ -391,16 +471,21 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
   for (int tb = 0; tb < kTokenBlocks; ++tb) {
     char *row = lds + (tb * 16 + r16) * kOutStride;
     if constexpr (kGated) {
+      // The activation is uniform over the launch: one branch, each side with its gate inlined.
+      auto gated = [&](auto activation) {
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        float v[4];
+        for (int jb = 0; jb < 2; ++jb) {
+          float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = gate(acc[tb][jb + 2][e], p.activation) * acc[tb][jb][e];
-        uint2 packed;
-        packed.x = pack_bf16x2(v[0], v[1]);
-        packed.y = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<uint2 *>(row + (wave * 32 + jb * 16 + 4 * g) * 2) = packed;
-      }
+          for (int e = 0; e < 4; ++e) v[e] = gate_of<decltype(activation)::value>(acc[tb][jb + 2][e]) * acc[tb][jb][e];
+          uint2 packed;
+          packed.x = pack_bf16x2(v[0], v[1]);
+          packed.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<uint2 *>(row + (wave * 32 + jb * 16 + 4 * g) * 2) = packed;
+        }
+      };
+      if (p.activation == UNISERVE_ACTIVATION_GELU_TANH) gated(std::integral_constant<int, UNISERVE_ACTIVATION_GELU_TANH>{});
+      else gated(std::integral_constant<int, UNISERVE_ACTIVATION_SILU>{});
     } else {
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
@@ -411,39 +496,91 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
       }
     }
   }
+  UNISERVE_E4M3_EPI_MARK(4);
   __syncthreads();
+  UNISERVE_E4M3_EPI_MARK(5);
+#ifdef UNISERVE_PROBE_NO_QUANT
+  if (kGated) return;
+#endif
   if (kGated && p.out_codes != nullptr) {
-    // Written as the FC2 operand: each (row, 128-column group) quantised by 16 lanes from the bf16
-    // values (the stand-alone quantiser's rounding points and encoding: amax of the bf16 values,
-    // s = amax / 448, code = e4m3(v / s)); live rows only.
+    // Written as the FC2 operand: each (row, 128-column group) quantised by 16 lanes (one DPP
+    // row) from the bf16 values (the stand-alone quantiser's rounding points and encoding: amax of
+    // the bf16 values, s = amax / 448, code = e4m3(v / s)); live rows only. Every lane's passes
+    // are independent: their LDS reads, reductions and encodings interleave.
     constexpr int kGroups = kOutCols / 128;
+    constexpr int kPasses = kRows * kGroups / (kThreads / 16);
+    static_assert(kRows * kGroups % (kThreads / 16) == 0, "whole passes");
     const int sub = t & 15;
     const int64_t groups_per_row = p.out_width / 128;
-    for (int index = t / 16; index < kRows * kGroups; index += kThreads / 16) {
+    float v[kPasses][8];
+    float amax[kPasses];
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int index = t / 16 + pass * (kThreads / 16);
       const int m = index / kGroups;
       const int group = index - m * kGroups;
       const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + (group * 128 + sub * 8) * 2);
-      float v[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        v[2 * j] = __uint_as_float(piece[j] << 16);
-        v[2 * j + 1] = __uint_as_float(piece[j] & 0xffff0000u);
+        v[pass][2 * j] = __uint_as_float(piece[j] << 16);
+        v[pass][2 * j + 1] = __uint_as_float(piece[j] & 0xffff0000u);
       }
-      float amax = 0.0f;
+      amax[pass] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+      for (int j = 0; j < 8; ++j) amax[pass] = __builtin_fmaxf(amax[pass], __builtin_fabsf(v[pass][j]));
+    }
 #pragma unroll
-      for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+    for (int pass = 0; pass < kPasses; ++pass) amax[pass] = row16_max(amax[pass]);
+    UNISERVE_E4M3_EPI_MARK(6);
+    // Every pass without division (e4m3_eight_bf16); the rare (row, group)s it leaves - a NaN,
+    // a scale outside its range - are encoded by division afterwards, from the staged tile, in
+    // one copy of that code.
+    uint32_t redo = 0;
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int index = t / 16 + pass * (kThreads / 16);
+      const int m = index / kGroups;
+      const int group = index - m * kGroups;
       if (m >= rows) continue;
-      const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+      const float scale = amax[pass] > 0.0f ? amax[pass] / 448.0f : 1.0f;
       const int64_t column = slice_col + group * 128 + sub * 8;
-      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(v, scale);
+      uint2 codes;
+      if (!e4m3_eight_bf16(v[pass], scale, codes)) redo |= 1u << pass;
+#ifdef UNISERVE_PROBE_NO_STORE
+      if (codes.x == 0x12345678u && codes.y == 0x9abcdef0u) p.out_codes[0] = 1;
+      if (sub == 0 && scale == 12345.0f) {
+#else
+      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = codes;
       if (sub == 0) {
+#endif
         const int64_t at = p.scale_rows != 0 ? column / 128 * p.scale_rows + first + m
                                              : (first + m) * groups_per_row + column / 128;
         p.out_code_scales[at] = scale;
       }
     }
+#pragma unroll 1
+    for (int pass = 0; pass < kPasses; ++pass) {
+      if (__ballot((redo >> pass) & 1u) == 0) continue;  // uniform: the whole wavefront redoes it
+      const int index = t / 16 + pass * (kThreads / 16);
+      const int m = index / kGroups;
+      const int group = index - m * kGroups;
+      const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + (group * 128 + sub * 8) * 2);
+      float w[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        w[2 * j] = __uint_as_float(piece[j] << 16);
+        w[2 * j + 1] = __uint_as_float(piece[j] & 0xffff0000u);
+      }
+      float wmax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wmax = __builtin_fmaxf(wmax, __builtin_fabsf(w[j]));
+      wmax = row16_max(wmax);
+      if (m >= rows || ((redo >> pass) & 1u) == 0) continue;
+      const float scale = wmax > 0.0f ? wmax / 448.0f : 1.0f;
+      const int64_t column = slice_col + group * 128 + sub * 8;
+      *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(w, scale);
+    }
+    UNISERVE_E4M3_EPI_MARK(2);
     return;
   }
   constexpr int kPieces = kOutCols / 8;
@@ -454,6 +591,7 @@ __global__ void __launch_bounds__(C::kWaves * kWave, C::kBlocksPerCU) e4m3_kerne
     const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + c * 16);
     *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
   }
+  UNISERVE_E4M3_EPI_MARK(2);
 }
 
 }  // namespace e4m3

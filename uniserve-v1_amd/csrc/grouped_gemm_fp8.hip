@@ -73,10 +73,10 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
-#pragma unroll
-    for (int offset = 8; offset > 0; offset >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, offset, 16));
+    amax = row16_max(amax);
     const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-    *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, scale);
+    *reinterpret_cast<uint2 *>(p.out + row * p.width + column) =
+        p.input_f32 ? e4m3_eight(v, scale) : e4m3_eight_of_bf16(v, scale);
     if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
     if (p.route_scales != nullptr) {
       for (int64_t k = sub; k < p.top; k += 16) {
@@ -735,3 +735,14 @@ int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, 
 }
 
 }  // namespace uniserve
+
+#ifdef UNISERVE_E4M3_TRACE
+extern "C" int uniserve_e4m3_trace_read(unsigned long long *out, int clear) {
+  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(e4m3_trace), sizeof(e4m3_trace)) != hipSuccess) return 1;
+  if (clear) {
+    static unsigned long long zeros[16384][8];
+    if (hipMemcpyToSymbol(HIP_SYMBOL(e4m3_trace), zeros, sizeof(zeros)) != hipSuccess) return 1;
+  }
+  return 0;
+}
+#endif
