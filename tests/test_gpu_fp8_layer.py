@@ -42,6 +42,41 @@ def test_quantiser_is_bit_exact(device):
     del q2, s2
 
 
+def magnitude_groups(rng):
+    """128-value groups that pair an amax with every bf16 magnitude not above it (random signs):
+    amax over every 4th mantissa of exponents across the range, the smallest subnormals and
+    the largest finite values included."""
+    exponents = [0, 1, 2, 3, 60, 100, *range(118, 137), 180, 250, 253, 254]
+    amaxes = [(e << 7) | m for e in exponents for m in range(0, 128, 4) if (e << 7) | m]
+    groups = []
+    for a in amaxes:
+        v = np.arange(0, a + 1, dtype=np.uint32)
+        v = v[v != a]
+        pad = (-len(v)) % 127
+        v = np.concatenate([v, np.zeros(pad, dtype=np.uint32)]).reshape(-1, 127)
+        g = np.concatenate([np.full((len(v), 1), a, dtype=np.uint32), v], axis=1)
+        groups.append(g)
+    bits = np.concatenate(groups).astype(np.uint16)
+    bits |= (rng.integers(0, 2, bits.shape, dtype=np.uint16) << 15)
+    rows = -(-len(bits) // 16)
+    out = np.zeros((rows * 16, 128), dtype=np.uint16)
+    out[:len(bits)] = bits
+    return out.reshape(rows, 2048)
+
+
+def test_quantiser_every_magnitude(device):
+    """The division-free quotients of the bf16 quantiser (shared with the FC1 epilogues) against
+    IEEE division, for every bf16 magnitude under each of ~1000 group maxima."""
+    announce("quantize fp8 every magnitude")
+    bits = magnitude_groups(np.random.default_rng(5))
+    x = torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16)
+    q, s = ops.quantize_fp8(x)
+    torch.cuda.synchronize()
+    want_q, want_s = O.quantize_rows_fp8(bits)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().numpy(), want_q)
+
+
 def quantized_stacks(device, experts, hidden, intermediate, seed=2):
     up_gate = normal_bf16((experts, 2 * intermediate, hidden), seed, 0.02, device)
     down = normal_bf16((experts, hidden, intermediate), seed + 1, 0.02, device)

@@ -57,12 +57,15 @@ __device__ __forceinline__ uint2 e4m3_eight(const float (&v)[8], float scale) {
 /// v / scale for a bf16 value v given r = 1 / scale, without a division: q0 = v r, then one
 /// correction by the residual v - q0 scale, exact under FMA (Markstein, IBM J. Res. Dev. 34(1),
 /// 1990). The result is within an ulp of the IEEE quotient and is not always equal to it, but its
-/// e4m3 code is: checked on the device over every pair of bf16 magnitudes v <= amax with
-/// scale = amax / 448 in [2^-100, 2^100] (5.3e8 pairs, no code differs).
+/// e4m3 code is, for scale = amax / 448 over bf16 values |v| <= amax: on the device, every pair of
+/// magnitudes with scale in [2^-100, 2^100] gives the code of the IEEE quotient (5.3e8 pairs; the
+/// operations are odd in v, and -0 keeps its sign), and the quantiser's GPU test repeats this with
+/// both signs for every magnitude under about a thousand maxima.
 __device__ __forceinline__ float quotient_bf16(float v, float scale, float r) {
   const float q0 = v * r;
   const float residual = __builtin_fmaf(-q0, scale, v);
-  return __builtin_fmaf(residual, r, q0);
+  // v = -0 gives q0 = -0 and a residual of +0, whose sum is +0: the sign is v's.
+  return __builtin_copysignf(__builtin_fmaf(residual, r, q0), v);
 }
 
 /// The e4m3 codes of two non-NaN values, packed into the low 16 bits, as e4m3_encode gives them:

@@ -33,6 +33,7 @@
 // The dot products over K use a permutation of K that both operands share, which changes only the
 // FP32 summation order.
 #include "common.hpp"
+#include "grouped_pair.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_route_gemm.h"
@@ -342,7 +343,7 @@ constexpr int64_t kStreamRowsPerExpert = 24;
 
 template <bool kGated>
 void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path, bool one_pass, hipStream_t s) {
-  if (!stream_path && prefill_fits<prefill::Bf16, kGated>(p.K, p.out_width)) {
+  if (!stream_path && (pair_fits<pair::Bf16>(kGated, p.K, p.out_width, 0) || prefill_fits<prefill::Bf16, kGated>(p.K, p.out_width))) {
     PrefillParams q{};
     q.act = reinterpret_cast<const uint8_t *>(p.act);
     q.weights = reinterpret_cast<const uint8_t *>(p.weights);
@@ -356,7 +357,8 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
     q.out_width = p.out_width;
     q.top = p.top;
     q.activation = p.activation;
-    launch_prefill<prefill::Bf16, kGated>(q, max_tiles, s);
+    if (pair_fits<pair::Bf16>(kGated, q.K, q.out_width, 0)) launch_pair<pair::Bf16>(q, kGated, max_tiles, s);
+    else launch_prefill<prefill::Bf16, kGated>(q, max_tiles, s);
     return;
   }
   const int64_t slices = kGated ? p.out_width / 64 : ceil_div<int64_t>(p.out_width, 128);

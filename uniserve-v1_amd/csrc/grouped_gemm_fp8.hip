@@ -16,7 +16,7 @@
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_dual.hpp"
-#include "grouped_e4m3.hpp"
+#include "grouped_pair.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_moe_fp8.h"
 
@@ -515,9 +515,9 @@ void launch_quantize_fp8_routes(const uint16_t *input, uint8_t *out, float *scal
 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream) {
-  // The 8-wave kernel with per-wave weight buffers first, then the two-workgroup kernel, then the
-  // 8-wave kernel of whole 256-K stage pairs, then the generic tiled kernel.
-  const bool fits = e4m3_fits(gated, p.K, p.out_width, p.scale_rows) || dual_fits(gated, p.K, p.out_width, p.out_codes != nullptr) ||
+  // The two-workgroup kernel first, then the 8-wave kernels (per-wave weight buffers of 256-K stage
+  // pairs, then the shared-stage one), then the generic tiled kernel.
+  const bool fits = pair_fits<pair::E4m3>(gated, p.K, p.out_width, p.scale_rows) || dual_fits(gated, p.K, p.out_width, p.out_codes != nullptr) ||
                     (gated ? prefill_fits<prefill::E4m3, true>(p.K, p.out_width)
                            : prefill_fits<prefill::E4m3, false>(p.K, p.out_width));
   if (!stream_path && fits) {
@@ -539,12 +539,10 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
     q.out_codes = p.out_codes;
     q.out_code_scales = p.out_code_scales;
     q.scale_rows = p.scale_rows;
-#ifndef UNISERVE_FP8_PREFILL_DUAL
-    if (e4m3_fits(gated, q.K, q.out_width, q.scale_rows)) {
-      launch_e4m3(q, gated, max_tiles, stream);
+    if (pair_fits<pair::E4m3>(gated, q.K, q.out_width, q.scale_rows)) {
+      launch_pair<pair::E4m3>(q, gated, max_tiles, stream);
       return;
     }
-#endif
     if (dual_fits(gated, q.K, q.out_width, q.out_codes != nullptr)) {
       launch_dual_e4m3(q, gated, max_tiles, stream);
       return;
@@ -735,14 +733,3 @@ int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, 
 }
 
 }  // namespace uniserve
-
-#ifdef UNISERVE_E4M3_TRACE
-extern "C" int uniserve_e4m3_trace_read(unsigned long long *out, int clear) {
-  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(e4m3_trace), sizeof(e4m3_trace)) != hipSuccess) return 1;
-  if (clear) {
-    static unsigned long long zeros[16384][8];
-    if (hipMemcpyToSymbol(HIP_SYMBOL(e4m3_trace), zeros, sizeof(zeros)) != hipSuccess) return 1;
-  }
-  return 0;
-}
-#endif
