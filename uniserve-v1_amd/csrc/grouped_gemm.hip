@@ -423,6 +423,15 @@ int32_t gather_gemm_bf16(const uniserve_gather_call *call, int32_t activation, v
   });
 }
 
+#ifdef UNISERVE_PAIR_TRACE
+extern "C" int uniserve_pair_trace_read_bf16(unsigned long long *out, int clear) {
+  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(pair_trace), sizeof(pair_trace)) != hipSuccess) return 1;
+  static unsigned long long zeros[16384][8];
+  if (clear && hipMemcpyToSymbol(HIP_SYMBOL(pair_trace), zeros, sizeof(zeros)) != hipSuccess) return 1;
+  return 0;
+}
+#endif
+
 }  // namespace uniserve
 
 extern "C" int32_t uniserve_gather_gemm(const uniserve_gather_call *call, void *stream) {

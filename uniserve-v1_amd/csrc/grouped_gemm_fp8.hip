@@ -732,4 +732,13 @@ int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, 
   });
 }
 
+#ifdef UNISERVE_PAIR_TRACE
+extern "C" int uniserve_pair_trace_read_fp8(unsigned long long *out, int clear) {
+  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(pair_trace), sizeof(pair_trace)) != hipSuccess) return 1;
+  static unsigned long long zeros[16384][8];
+  if (clear && hipMemcpyToSymbol(HIP_SYMBOL(pair_trace), zeros, sizeof(zeros)) != hipSuccess) return 1;
+  return 0;
+}
+#endif
+
 }  // namespace uniserve

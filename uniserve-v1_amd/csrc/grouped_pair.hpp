@@ -36,6 +36,20 @@
 #include "grouped_fp8.hpp"
 #include "grouped_prefill.hpp"
 
+#ifdef UNISERVE_PAIR_TRACE
+// Development timing of each workgroup (s_memrealtime at its start, loop start, loop end and end;
+// HW_ID), read back by the trace entries of builds made with this macro only.
+static __device__ unsigned long long pair_trace[16384][8];
+#define UNISERVE_PAIR_MARK(slot)                                                                           \
+  do {                                                                                                     \
+    if (threadIdx.x == 0 && blockIdx.x < 16384) pair_trace[blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define UNISERVE_PAIR_MARK(slot) \
+  do {                           \
+  } while (0)
+#endif
+
 namespace uniserve {
 namespace pair {
 
@@ -144,6 +158,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   const int tile = first_tile + within % in_group;
   if (tile >= p.num_tiles[0]) return;
 
+  UNISERVE_PAIR_MARK(0);
   const int64_t expert = p.tile_to_expert[tile];
   const int64_t first = static_cast<int64_t>(tile) * kRows;
   const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
@@ -263,6 +278,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   issue_act(1, 0);
   issue_act(1, 1);
   if constexpr (F::kScaled) wait_loads_and_scales<kLast>(sx);
+  UNISERVE_PAIR_MARK(1);
   for (int k = 0; k < stages; ++k) {
     prefill::wait_loads_but<kLast>();
     __syncthreads();
@@ -346,6 +362,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   }
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done with the operand buffers
+  UNISERVE_PAIR_MARK(2);
 
   // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row 16 tb + r16
   // and the wave's weight rows 16 jb + 4 g + e in element e. The output tile goes through LDS so
@@ -454,6 +471,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
       const int64_t column = slice_col + group * 128 + sub * 8;
       *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(w, scale);
     }
+    UNISERVE_PAIR_MARK(3);
     return;
   }
   constexpr int kPieces = kOutCols / 8;
@@ -464,6 +482,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
     const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + c * 16);
     *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
   }
+  UNISERVE_PAIR_MARK(3);
 }
 
 }  // namespace pair
@@ -481,8 +500,11 @@ inline bool pair_fits(bool gated, int64_t K, int64_t out_width, int64_t scale_ro
 
 /// Launches it over `max_tiles` tiles (tiles past `num_tiles` exit at once); with `p.out_codes`
 /// set (e4m3 FC1 only) the gated rows are written as e4m3 codes and scales.
+#ifndef UNISERVE_PAIR_GROUP
+#define UNISERVE_PAIR_GROUP 4
+#endif
 template <class F>
-inline void launch_pair(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream, int group = 4) {
+inline void launch_pair(PrefillParams p, bool gated, int64_t max_tiles, hipStream_t stream, int group = UNISERVE_PAIR_GROUP) {
   const int64_t columns = gated ? pair::kSliceRows / 2 : pair::kSliceRows;
   p.slices = static_cast<int32_t>(p.out_width / columns);
   p.max_tiles = static_cast<int32_t>(max_tiles);
