@@ -71,6 +71,14 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   // eight K elements at 8 (l / 16); rows past the edge read row 0 and are never stored.
   const int64_t m = static_cast<int64_t>(blockIdx.x) * kTile + r16;
   const int64_t n = static_cast<int64_t>(blockIdx.y) * kTile + r16;
+  // Wave 0's lanes add the bias of experts 4 (l / 16) .. + 3 of the tile: loaded now, with the
+  // operands, rather than after the reduction.
+  float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (wave == 0 && p.bias != nullptr) {
+    const int64_t col = static_cast<int64_t>(blockIdx.y) * kTile + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[i] = col + i < p.experts ? p.bias[col + i] : 0.0f;
+  }
   const uint16_t *x_row = p.x + (m < p.tokens ? m : 0) * p.hidden + g * 8;
   const uint16_t *w_row = p.w + (n < p.experts ? n : 0) * p.hidden + g * 8;
   floatx4 acc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -106,7 +114,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
       for (int i = 0; i < 4; ++i) {
         if (col + i >= p.experts) continue;
         float v = total[i];
-        if (p.bias != nullptr) v += p.bias[col + i];
+        if (p.bias != nullptr) v += bias[i];
         p.scores[row * p.experts + col + i] = f32_to_bf16(v);
       }
     }
