@@ -249,7 +249,7 @@ def traffic_summary(directory):
     import re
 
     products = {"gather_gemm": "true", "route_gemm": "false"}
-    pattern = re.compile(r"((?:stream|prefill|tiled|e4m3)\w*)<([^<>]*)>\(")
+    pattern = re.compile(r"((?:stream|prefill|tiled|pair)\w*)<([^<>]*)>\(")
     configs = {}
     for name in CONFIGS:
         if not (root / name).exists():
@@ -258,9 +258,9 @@ def traffic_summary(directory):
         write = counter_means(root / name / "write", "WRITE_SIZE")
         entry = {}
         for product, gated in products.items():
-            def gated_flag(match):  # prefill_kernel<format, gated>; every other kernel <gated, ...>
+            def gated_flag(match):  # prefill_kernel / pair_kernel<format, gated>; the others <gated, ...>
                 args = [a.strip() for a in match.group(2).split(",")]
-                return args[-1] if match.group(1).startswith("prefill") else args[0]
+                return args[-1] if match.group(1).startswith(("prefill", "pair")) else args[0]
 
             found = [(k, m) for k, m in ((k, pattern.search(k)) for k in fetch) if m and gated_flag(m) == gated]
             if not found:
