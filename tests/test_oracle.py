@@ -27,7 +27,18 @@ fp8 quantisers              dequantisation error within half an e4m3 step; block
                             dequantised values (the format has no reference: parity with the
                             reference is unpinned, the arithmetic is pinned)
 moe_layer                   float64 composition of the pieces above on the tiny config;
-                            invariance under a redistribution of the experts
+                            invariance under a redistribution of the experts; the routing options
+                            (router bias, slot map, load counts, expert window, live tokens) against
+                            a float64 layer written from the reference tests' hand loops
+router bias                 float64 brute force of x.W + b with one rounding; a crafted case where
+                            rounding before the bias gives another bf16 value
+gate (silu, gelu_tanh)      float64 closed forms and torch's gelu(approximate='tanh')
+fp32 layer     float64 composition: ids equal, outputs within the reference tests'
+                            FP32 tolerance
+MX quantisers, products     E2M1 codes by brute force with ties to even; the E8M0 scale by its two
+                            defining inequalities; MXFP8 against torch's e4m3 cast; float64 sums
+                            of dequantised values (parity with the reference unpinned: NVFP4)
+sigmoid_gated_add           the reference's own case (moe.rs:1865-1886); one rounding per type
 ==========================  ====================================================================
 """
 
