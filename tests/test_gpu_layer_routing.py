@@ -148,10 +148,22 @@ def test_gelu_tanh_fc1_against_the_oracle(device, case):
     assert (a != b).mean() > 0.5
 
 
-@pytest.mark.parametrize("wdtype", ["bf16", "f8e4m3", "f4e2m1"])
-def test_layer_with_the_gelu_tanh_gate(device, wdtype):
-    tokens, hidden, experts, top, intermediate = 64, 2048, 128, 8, 768
-    announce("layer gelu_tanh", wdtype)
+GELU_LAYERS = {
+    # name: weights, tokens, hidden, experts, top, intermediate
+    "bf16 decode": ("bf16", 64, 2048, 128, 8, 768),
+    "f8e4m3 decode": ("f8e4m3", 64, 2048, 128, 8, 768),
+    "f4e2m1 decode": ("f4e2m1", 64, 2048, 128, 8, 768),
+    # 128 routes per expert: the prefill products (the two-workgroup kernels, e4m3 FC1 writing
+    # FC2's operand through its division-free quantiser)
+    "bf16 prefill": ("bf16", 512, 1024, 32, 8, 512),
+    "f8e4m3 prefill": ("f8e4m3", 512, 1024, 32, 8, 512),
+}
+
+
+@pytest.mark.parametrize("case", list(GELU_LAYERS))
+def test_layer_with_the_gelu_tanh_gate(device, case):
+    wdtype, tokens, hidden, experts, top, intermediate = GELU_LAYERS[case]
+    announce("layer gelu_tanh", case)
     x = normal_bf16((tokens, hidden), 81, device=device)
     router = normal_bf16((experts, hidden), 82, 0.02, device)
     up_gate = normal_bf16((experts, 2 * intermediate, hidden), 83, 0.02, device)
@@ -163,7 +175,7 @@ def test_layer_with_the_gelu_tanh_gate(device, wdtype):
     want_bits, want_ids, _, _ = O.moe_layer(bf16_bits(x), bf16_bits(router), w1, w2, top, up_gate_scales=s1,
                                             down_scales=s2, activation=1)
     np.testing.assert_array_equal(layer.view("ids", torch.int32, (tokens, top)).cpu().numpy(), want_ids)
-    assert_bf16_bar(bf16_values(out), O.bf16_decode(want_bits), f"layer gelu_tanh {wdtype}",
+    assert_bf16_bar(bf16_values(out), O.bf16_decode(want_bits), f"layer gelu_tanh {case}",
                     max_rel=2e-2 if wdtype == "bf16" else 4e-2)
 
 

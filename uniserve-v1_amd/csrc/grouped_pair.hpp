@@ -260,7 +260,8 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   // ---- the K loop. Prefetched during stage k: the wave's weights of stage k + 1 (it has read
   // stage k's into registers at the top), the scales of stage k + 1 and the activations of stage
   // k + 2 (into the slot stage k - 1 used: every wavefront has passed the barrier after reading
-  // it); past the last stage, the last stage again (cache-resident, into buffers nobody reads), so
+  // it); past the last stage, the last stage again (cache-resident: into buffers nobody reads, or,
+  // in the second-to-last stage, over the last stage's activation rows with the same bytes), so
   // that every wait counts alike. They go out in that order - weights, scales, activations. At the
   // end of stage k everything up to the scales of stage k + 1 has landed (the wait that makes the
   // scale registers readable), at the top of stage k + 1 everything but the activations, then
