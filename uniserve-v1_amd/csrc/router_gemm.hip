@@ -24,16 +24,24 @@ constexpr int kDepth = 8;  // K steps whose loads are in flight
 
 __device__ __forceinline__ int swizzled(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
 
+/// kBMTile: tokens per workgroup (64: four waves of 16 tokens x 64 experts; 32: waves of 16
+/// tokens x 32 experts, twice the workgroups for the same batch).
+template <int kBMTile>
 __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) {
-  __shared__ u32x4 shared_x[2][kBM * 8];
+  constexpr int kXLoads = kBMTile / 32;           // x rows per thread and step
+  constexpr int kColBlocks = kBMTile == 64 ? 4 : 2;  // 16-expert blocks per wave
+  __shared__ u32x4 shared_x[2][kBMTile * 8];
   __shared__ u32x4 shared_w[2][kBN * 8];
   const int t = static_cast<int>(threadIdx.x);
   const int wave = t / kWave;
   const int lane = lane_id();
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBM;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBMTile;
   const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kBN;
+  // The wave's 16 tokens and first expert of the tile.
+  const int wave_m = kBMTile == 64 ? wave * 16 : (wave & 1) * 16;
+  const int wave_n = kBMTile == 64 ? 0 : (wave >> 1) * 32;
 
   const int chunk = t & 7;
   const uint16_t *x_row[2];
@@ -42,24 +50,25 @@ __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) 
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = (t >> 3) + 32 * i;
-    x_valid[i] = m0 + r < p.m;
+    x_valid[i] = i < kXLoads && m0 + r < p.m;
     w_valid[i] = n0 + r < p.n;
     x_row[i] = p.x + (x_valid[i] ? m0 + r : 0) * p.x_stride + chunk * 8;
     w_row[i] = p.w + (w_valid[i] ? n0 + r : 0) * p.w_stride + chunk * 8;
   }
-  floatx4 acc[4];
+  floatx4 acc[kColBlocks];
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) acc[ni] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int ni = 0; ni < kColBlocks; ++ni) acc[ni] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // The K steps' global loads run kDepth steps ahead in registers (the MFMA work of a step is far
   // shorter than a load's latency); each step goes through one of two LDS buffers, one barrier
   // per step.
   const int64_t steps = p.k / kBK;
-  u32x4 rx[kDepth][2], rw[kDepth][2];
+  u32x4 rx[kDepth][kXLoads], rw[kDepth][2];
   auto load = [&](int d, int64_t step) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      rx[d][i] = x_valid[i] ? *reinterpret_cast<const u32x4 *>(x_row[i] + step * kBK) : u32x4{0, 0, 0, 0};
+      if (i < kXLoads)
+        rx[d][i] = x_valid[i] ? *reinterpret_cast<const u32x4 *>(x_row[i] + step * kBK) : u32x4{0, 0, 0, 0};
       rw[d][i] = w_valid[i] ? *reinterpret_cast<const u32x4 *>(w_row[i] + step * kBK) : u32x4{0, 0, 0, 0};
     }
   };
@@ -75,7 +84,7 @@ __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) 
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int r = (t >> 3) + 32 * i;
-        shared_x[buffer][swizzled(r, chunk)] = rx[d][i];
+        if (i < kXLoads) shared_x[buffer][swizzled(r, chunk)] = rx[d][i];
         shared_w[buffer][swizzled(r, chunk)] = rw[d][i];
       }
       __syncthreads();
@@ -83,21 +92,21 @@ __global__ void __launch_bounds__(kRouterThreads) router_kernel(RouterParams p) 
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int c = ks * 4 + g;
-        const u32x4 xf = shared_x[buffer][swizzled(wave * 16 + r16, c)];
+        const u32x4 xf = shared_x[buffer][swizzled(wave_m + r16, c)];
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
-          const u32x4 wf = shared_w[buffer][swizzled(ni * 16 + r16, c)];
+        for (int ni = 0; ni < kColBlocks; ++ni) {
+          const u32x4 wf = shared_w[buffer][swizzled(wave_n + ni * 16 + r16, c)];
           acc[ni] = mfma_16x16x32_bf16(wf, xf, acc[ni]);
         }
       }
     }
   }
 
-  const int64_t m = m0 + wave * 16 + r16;
+  const int64_t m = m0 + wave_m + r16;
   if (m >= p.m) return;
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    const int64_t n = n0 + ni * 16 + 4 * g;
+  for (int ni = 0; ni < kColBlocks; ++ni) {
+    const int64_t n = n0 + wave_n + ni * 16 + 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (n + i >= p.n) continue;
@@ -171,9 +180,13 @@ void launch_router(const RouterParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(skinny_router_kernel, grid, dim3(kSkinnyWaves * kWave), 0, stream, p);
     return;
   }
-  const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.m, kBM)),
+#ifndef UNISERVE_ROUTER_BM
+#define UNISERVE_ROUTER_BM 32
+#endif
+  constexpr int kTileM = UNISERVE_ROUTER_BM;
+  const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.m, kTileM)),
                   static_cast<uint32_t>(ceil_div<int64_t>(p.n, kBN)));
-  hipLaunchKernelGGL(router_kernel, grid, dim3(kRouterThreads), 0, stream, p);
+  hipLaunchKernelGGL(router_kernel<kTileM>, grid, dim3(kRouterThreads), 0, stream, p);
 }
 
 }  // namespace uniserve
