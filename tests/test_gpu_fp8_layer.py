@@ -143,6 +143,10 @@ LAYERS = {
     "235b decode fp8 one token": (1, 4096, 128, 8, 1536, "f8e4m3", False, None),
     # the two-workgroup e4m3 kernels at 235B width, route-major scales
     "235b prefill fp8 zipf": (4096, 4096, 128, 8, 1536, "f8e4m3", True, 64),
+    # the two-workgroup kernels at their fewest stages (three: e4m3 H = 384, bf16 H = 192), ragged
+    # tiles; FC2 of these widths takes the other prefill kernels
+    "small prefill fp8, three-stage FC1": (600, 384, 8, 2, 256, "f8e4m3", True, None),
+    "small prefill bf16, three-stage FC1": (600, 192, 8, 2, 128, "bf16", True, None),
 }
 
 
