@@ -226,14 +226,14 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
     asm volatile("" ::"v"(sw_lanes[0]), "v"(sw_lanes[1]));
   }
 
-  // Weights of stage k, instructions 4 h .. 4 h + 3; `after_reads`: the wave just read its rows of
-  // the buffer, and the first DMA waits for those LDS reads (lgkmcnt 0) before it may overwrite
-  // them.
-  auto issue_weights = [&](int k, int h, bool after_reads) {
+  // Weights of stage k, the h-th of `parts` equal runs of the eight instructions; `after_reads`:
+  // the wave just read its rows of the buffer, and the first DMA waits for those LDS reads
+  // (lgkmcnt 0) before it may overwrite them.
+  auto issue_weights = [&](int k, int h, bool after_reads, int parts = 2) {
     const uint32_t weight_lds = lds_address(sh.weights[wave]);
 #pragma unroll
-    for (int j = 0; j < kWeightLoads / 2; ++j) {
-      const int i = h * (kWeightLoads / 2) + j;
+    for (int j = 0; j < kWeightLoads / parts; ++j) {
+      const int i = h * (kWeightLoads / parts) + j;
       const uint8_t *base = w_base[i / 4] + static_cast<int64_t>(k) * 128 + static_cast<int64_t>(i % 4) * 8 * row_bytes;
       const uint32_t lane_offset = w_lane + ((w_chunk ^ static_cast<uint32_t>(4 * (i & 1))) << 4);
       const uint32_t dst = __builtin_amdgcn_readfirstlane(weight_lds + i * kWave * 16);
@@ -289,16 +289,17 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
     for (int jb = 0; jb < 4; ++jb) wf[jb] = fragment(sh.weights[wave], jb * 16 + r16, g);
     const int act_next = min(k + 2, stages - 1);
     const int next = min(k + 1, stages - 1);
-    // The loads issued before token block tb's MFMAs.
+    // The loads issued before token block tb's MFMAs: two weight instructions before each of the
+    // first four blocks, then the scales, then the activations.
     auto issue_part = [&](int tb) {
-      if (tb == 0) issue_weights(next, 0, true);
-      if (tb == 1) issue_weights(next, 1, false);
+      if (tb < 4) issue_weights(next, tb, tb == 0, 4);
+      constexpr int kActAt = F::kScaled ? 6 : 4;
       if constexpr (F::kScaled) {
-        if (tb == 2) load_scales_half<0>(sx, scale_table + next * sx_stage, sx_off);
-        if (tb == 3) load_scales_half<1>(sx, scale_table + next * sx_stage, sx_off);
+        if (tb == 4) load_scales_half<0>(sx, scale_table + next * sx_stage, sx_off);
+        if (tb == 5) load_scales_half<1>(sx, scale_table + next * sx_stage, sx_off);
       }
-      if (tb == 4) issue_act(act_next, 0);
-      if (tb == 5) issue_act(act_next, 1);
+      if (tb == kActAt) issue_act(act_next, 0);
+      if (tb == kActAt + 1) issue_act(act_next, 1);
     };
 
     if constexpr (F::kScaled) {
