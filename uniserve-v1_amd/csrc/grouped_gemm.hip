@@ -103,10 +103,24 @@ __device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
 }
 
 /// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
+// Development timing of each workgroup (s_memrealtime at its start, after its first stage and at
+// its end), in builds made with UNISERVE_PAIR_TRACE only.
+#ifdef UNISERVE_PAIR_TRACE
+#define STREAM_MARK(slot)                                                                                  \
+  do {                                                                                                     \
+    const unsigned lin = blockIdx.x + blockIdx.y * gridDim.x;                                              \
+    if (threadIdx.x == 0 && lin < 16384) pair_trace[lin][slot] = __builtin_amdgcn_s_memrealtime();         \
+  } while (0)
+#else
+#define STREAM_MARK(slot) \
+  do {                    \
+  } while (0)
+#endif
 template <bool kGated, int kPassTiles>
 __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   const int tile = static_cast<int>(blockIdx.x);
   if (tile >= p.num_tiles[0]) return;
+  STREAM_MARK(0);
   const int64_t expert = p.tile_to_expert[tile];
   const int64_t first = static_cast<int64_t>(tile) * kTileRows;
   const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
@@ -192,6 +206,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
     for (int k = 0; k < stages; k += 2) {
       if (k + 1 < stages) load(odd, k + 1);
       compute(even);
+      if (k == 0) STREAM_MARK(1);
       if (k + 2 < stages) load(even, k + 2);
       if (k + 1 < stages) compute(odd);
     }
@@ -212,6 +227,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
       }
     }
   }
+  STREAM_MARK(3);
 }
 
 // ---- tiled kernel -----------------------------------------------------------------------------------------
