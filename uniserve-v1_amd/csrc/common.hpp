@@ -108,6 +108,18 @@ __device__ __forceinline__ float gate(float g, int32_t activation) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
 }
 
+/// Device-scope loads and stores (relaxed agent-scope atomics: they reach the GPU's coherence point,
+/// past the per-XCD L2 slices, with no cache write-back or invalidation) - for values one
+/// workgroup hands another inside one launch.
+template <class T>
+__device__ __forceinline__ T load_device(const T *pointer) {
+  return __hip_atomic_load(pointer, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void store_device(T *pointer, T value) {
+  __hip_atomic_store(pointer, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- MFMA operands ------------------------------------------------------------------------------------
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -7,9 +7,10 @@
 //
 // Every workgroup computes one 16-token x 16-expert tile of scores, its contraction split over 16
 // wavefronts (partial sums added in wavefront order, the bias added to the FP32 sum, one rounding
-// into bf16), and stores it. Then two rounds of tickets - agent-scope atomic counters with
-// release/acquire ordering, so a taker of a round's last ticket sees everything the round's
-// other workgroups stored:
+// into bf16), and stores it. Then two rounds of tickets - agent-scope atomic counters; the scores
+// and ids that cross workgroups are stored and read at device scope (past the per-XCD L2 slices),
+// and a workgroup counts only after its stores have completed, so a taker of a round's last ticket
+// reads everything the round's other workgroups stored, with no cache write-back or invalidation:
 //   * the last of a token block's workgroups routes that block's 16 tokens (the topk routine of
 //     topk_route.hpp, one token per 32-lane half: ids and weights bit for bit those of the
 //     topk_softmax kernel) - the routing is spread over the token blocks' CUs, since on one CU its
@@ -42,20 +43,21 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kUnroll = 4;                    // K steps of 32 whose loads a wavefront keeps in flight
 constexpr int kTile = 16;
 
-/// Takes a ticket of `counter` for one of `takers` workgroups (thread 0; the workgroup's stores
-/// ordered before it by the caller's barrier); answers, to every thread, whether it was the last,
-/// and then the counter is reset and every taker's stores are visible to this workgroup.
+/// Takes a ticket of `counter` for one of `takers` workgroups; answers, to every thread, whether it
+/// was the last (then the counter is reset). What crosses workgroups - the scores and the ids - is
+/// stored and read at device scope, so a ticket needs no cache maintenance: every thread's stores
+/// have completed (vmcnt counts stores) before the workgroup's barrier and thread 0's count.
 __device__ __forceinline__ bool last_ticket(uint32_t *counter, uint32_t takers, int32_t *flag) {
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t taken = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t taken = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = taken + 1 == takers;
     if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = last ? 1 : 0;
   }
   __syncthreads();
-  if (*flag == 0) return false;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  return true;
+  return *flag != 0;
 }
 
 __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
@@ -115,7 +117,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
         if (col + i >= p.experts) continue;
         float v = total[i];
         if (p.bias != nullptr) v += bias[i];
-        p.scores[row * p.experts + col + i] = f32_to_bf16(v);
+        store_device(p.scores + row * p.experts + col + i, f32_to_bf16(v));
       }
     }
   }
@@ -128,7 +130,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   if (half < kTile) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kTile + half;
     const bool active = row < p.tokens;
-    topk::route_token(p.scores, 1, p.experts, static_cast<int>(active ? row : 0), static_cast<int>(p.experts), p.top,
+    topk::route_token<true>(p.scores, 1, p.experts, static_cast<int>(active ? row : 0), static_cast<int>(p.experts), p.top,
                       p.renormalize, nullptr, -1, p.ids, p.weights, p.map, p.live, p.load, active);
   }
   __syncthreads();
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   // 3. The last of the token blocks sorts every route.
   if (!last_ticket(p.ticket, gridDim.x, &flag)) return;
   UNISERVE_TRACE(4);
-  sort::small_sort<false>(p.sort, front_lds);
+  sort::small_sort<false, true>(p.sort, front_lds);
   UNISERVE_TRACE(3);
 }
 

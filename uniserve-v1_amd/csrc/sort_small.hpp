@@ -32,10 +32,13 @@ struct SortParams {
   int32_t key_bits;  ///< bits of (local expert + 1), the match key
 };
 
-/// The local expert of route `route`, or -1 when it is not live or not in the window.
+/// The local expert of route `route`, or -1 when it is not live or not in the window. kDevice: `ids`
+/// read at device scope (stored by other workgroups of the launch).
+template <bool kDevice = false>
 __device__ __forceinline__ int32_t local_expert(const SortParams &p, int64_t route, int64_t live) {
   if (route >= p.routes || route >= live) return -1;
-  const int64_t local = static_cast<int64_t>(p.ids[route]) - p.local_offset;
+  const int32_t id = kDevice ? load_device(p.ids + route) : p.ids[route];
+  const int64_t local = static_cast<int64_t>(id) - p.local_offset;
   return (local >= 0 && local < p.local_experts) ? static_cast<int32_t>(local) : -1;
 }
 
@@ -58,8 +61,9 @@ __host__ __device__ constexpr int64_t small_sort_lds_words(int64_t local_experts
 
 /// The whole sort by one workgroup of kSortThreads threads; `lds` holds
 /// small_sort_lds_words(local experts) words. Without kPadding the padding rows of a tile (past its
-/// expert's routes) are left unwritten in permuted_to_expanded and permuted_to_token.
-template <bool kPadding>
+/// expert's routes) are left unwritten in permuted_to_expanded and permuted_to_token. kDeviceIds:
+/// `ids` read at device scope.
+template <bool kPadding, bool kDeviceIds = false>
 __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
   const int E = p.local_experts;
   int32_t *rows = lds;                          // [kSortWaves][E] counts, then start rows
@@ -82,7 +86,7 @@ __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
   for (int u = 0; u < kSmallGroups; ++u) {
     const int64_t route = (first_group + u) * kWave + lane;
     inside[u] = u < own && route < p.routes;
-    e[u] = inside[u] ? local_expert(p, route, live) : -1;
+    e[u] = inside[u] ? local_expert<kDeviceIds>(p, route, live) : -1;
   }
 #pragma unroll
   for (int u = 0; u < kSmallGroups; ++u) peers[u] = match_any(static_cast<uint32_t>(e[u] + 1), p.key_bits);

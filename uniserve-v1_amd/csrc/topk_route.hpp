@@ -86,6 +86,13 @@ __device__ __forceinline__ float load_kind(const void *data, int kind, int64_t i
   if (kind == 2) return static_cast<float>(static_cast<const _Float16 *>(data)[index]);
   return bf16_to_f32(static_cast<const uint16_t *>(data)[index]);
 }
+/// The same read at device scope (scores another workgroup of the launch stored at device scope).
+__device__ __forceinline__ float load_kind_device(const void *data, int kind, int64_t index) {
+  if (kind == 0) return load_device(static_cast<const float *>(data) + index);
+  const uint16_t bits = load_device(static_cast<const uint16_t *>(data) + index);
+  if (kind == 2) return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+  return bf16_to_f32(bits);
+}
 
 template <int kOffset>
 __device__ __forceinline__ void max_step(float &maximum) {
@@ -109,8 +116,9 @@ __device__ __forceinline__ void argmax_step(float &best, int &expert) {
 }
 
 /// Routes one token with `kIter` scores per lane (the expert count in whole halves, rounded up to
-/// a power of two: the extra slots hold -inf and add exact zeros to the sum).
-template <int kIter>
+/// a power of two: the extra slots hold -inf and add exact zeros to the sum). kDevice: the scores
+/// are read and the ids stored at device scope (scores and ids cross workgroups of one launch).
+template <int kIter, bool kDevice>
 __device__ __forceinline__ void route(const void *scores, int score_kind, int64_t row_stride,
                                       int row, int experts, int top, int renormalize,
                                       const void *scale, int scale_kind, int32_t *ids,
@@ -121,9 +129,9 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
 #pragma unroll
   for (int it = 0; it < kIter; ++it) {
     const int expert = lane + it * kHalf;
-    values[it] = expert < experts
-                     ? load_kind(scores, score_kind, static_cast<int64_t>(row) * row_stride + expert)
-                     : -__builtin_inff();
+    const int64_t at = static_cast<int64_t>(row) * row_stride + expert;
+    values[it] = expert < experts ? (kDevice ? load_kind_device(scores, score_kind, at) : load_kind(scores, score_kind, at))
+                                  : -__builtin_inff();
   }
 
   UNISERVE_TRACE(20);
@@ -210,7 +218,9 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
   const bool named = picked_expert >= 0 && picked_expert < experts;
   if (scale_kind != -1 && scale != nullptr && named) weight = weight * load_kind(scale, scale_kind, picked_expert);
   const int64_t slot = static_cast<int64_t>(row) * top + lane;
-  ids[slot] = (map != nullptr && named) ? map[picked_expert] : picked_expert;
+  const int32_t id = (map != nullptr && named) ? map[picked_expert] : picked_expert;
+  if constexpr (kDevice) store_device(ids + slot, id);
+  else ids[slot] = id;
   weights[slot] = weight;
   if (load != nullptr && named && (live == nullptr || row < live[0])) atomicAdd(load + picked_expert, 1ull);
 }
@@ -218,23 +228,24 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
 
 /// Routes token `row` (`active` false: take part in the wavefront's exchanges, store nothing),
 /// with the per-lane slot count the expert count needs.
+template <bool kDevice = false>
 __device__ __forceinline__ void route_token(const void *scores, int score_kind, int64_t row_stride, int row,
                                             int experts, int top, int renormalize, const void *scale,
                                             int scale_kind, int32_t *ids, float *weights, const int32_t *map,
                                             const int32_t *live, unsigned long long *load, bool active) {
   const int needed = (experts + kHalf - 1) / kHalf;
   if (needed <= 1)
-    route<1>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<1, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
   else if (needed <= 2)
-    route<2>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<2, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
   else if (needed <= 4)
-    route<4>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<4, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
   else if (needed <= 8)
-    route<8>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<8, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
   else if (needed <= 16)
-    route<16>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<16, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
   else
-    route<32>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<32, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
 }
 
 }  // namespace topk
