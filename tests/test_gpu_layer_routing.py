@@ -42,6 +42,8 @@ ROUTED = {
     "mx decode, map + load + window": (64, 2048, 128, 8, 768, "f4e2m1", (64, 64), None),
     "mx prefill, map + load + window": (2048, 2048, 128, 8, 768, "f4e2m1", (8, 112), None),
     "bf16 decode, every expert, map + load only": (64, 2048, 128, 8, 768, "bf16", None, None),
+    "bf16 decode, map + load + window + live": (64, 2048, 128, 8, 768, "bf16", (40, 64), 50),
+    "bf16 one token, map + load + window": (1, 2048, 128, 8, 768, "bf16", (32, 64), None),
 }
 
 

@@ -1,0 +1,32 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The layer's bf16 decode products without a sort (grouped_gemm.hip): each stream workgroup serves
+// one local expert and finds that expert's routes in `ids` itself; rows sit at their expanded
+// positions (route t * top + k), so the combine reads them in the expanded layout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace uniserve {
+
+struct ExpertStream {
+  const void *act;           ///< FC1: hidden [tokens, K]; FC2: gated rows [routes, K]
+  const void *weights;       ///< [local experts, n_total, K] bf16
+  void *out;                 ///< [routes, out_width] bf16, rows at expanded positions
+  const int32_t *ids;        ///< [routes] expert ids after the slot map
+  const int32_t *live_tokens;///< [1] or null
+  int64_t routes, top, local_offset, local_experts;
+  int64_t K, n_total, out_width;
+  int32_t activation;        ///< FC1's gate
+};
+
+/// Whether the expert-major stream kernel serves these extents (decode batches: at most 4096
+/// routes, few per expert; FC1 widths of whole 64-column slices, FC2 of whole 128-column ones).
+bool expert_stream_fits(int64_t routes, int64_t local_experts, int64_t K, int64_t out_width, bool gated);
+
+/// FC1 (`gated`: the gate of `activation` times the up half) or FC2 over the listed routes.
+void launch_expert_stream(const ExpertStream &e, bool gated, hipStream_t stream);
+
+}  // namespace uniserve

@@ -34,6 +34,7 @@
 // FP32 summation order.
 #include "common.hpp"
 #include "grouped_pair.hpp"
+#include "expert_stream.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_gather_gemm.h"
 #include "uniserve_route_gemm.h"
@@ -43,6 +44,7 @@ namespace {
 
 constexpr int kTileRows = 128;
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
 
 struct GroupedParams {
   const uint16_t *act;      ///< FC1: hidden [tokens, K]; FC2: rows [permuted_rows, K]
@@ -57,6 +59,12 @@ struct GroupedParams {
   int64_t out_width;        ///< I (FC1) or H (FC2)
   int64_t top;
   int32_t activation;       ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
+  // Expert-major stream (decode, no sort): workgroup x serves local expert x; its rows are the
+  // routes naming it, found in `ids`, in route order, at their expanded positions.
+  const int32_t *ids;       ///< [routes] expert ids (after the slot map)
+  const int32_t *live_tokens;
+  int64_t routes;
+  int64_t local_offset;
 };
 
 __device__ __forceinline__ u32x4 load16(const uint16_t *pointer) {
@@ -116,18 +124,35 @@ __device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
   do {                    \
   } while (0)
 #endif
-template <bool kGated, int kPassTiles>
+/// Most routes one expert-major workgroup serves (the routes of a decode batch).
+constexpr int kExpertRoutes = 4096;
+constexpr int kScanChunk = kWave;
+
+/// kByExpert: workgroup x serves local expert x (grid: local experts x slices) and finds its rows
+/// itself - the routes whose id is the expert's, in route order, live ones only (each wavefront
+/// ballots a quarter of the routes into a list in LDS) - while its first weight stage is in
+/// flight; FC1 reads token route / top and FC2 row `route`, and both write row `route` (the
+/// expanded layout). Otherwise the sort's tile tables give the tile's expert and rows.
+template <bool kGated, int kPassTiles, bool kByExpert = false>
 __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
-  const int tile = static_cast<int>(blockIdx.x);
-  if (tile >= p.num_tiles[0]) return;
-  STREAM_MARK(0);
-  const int64_t expert = p.tile_to_expert[tile];
-  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
-  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int r16 = lane & 15;
   const int g = lane >> 4;
+  int64_t expert, first;
+  int rows;
+  if constexpr (kByExpert) {
+    expert = blockIdx.x;
+    first = 0;
+    rows = 0;
+  } else {
+    const int tile = static_cast<int>(blockIdx.x);
+    if (tile >= p.num_tiles[0]) return;
+    expert = p.tile_to_expert[tile];
+    first = static_cast<int64_t>(tile) * kTileRows;
+    rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  }
+  STREAM_MARK(0);
 
   int64_t n0, n1;
   if constexpr (kGated) {
@@ -136,7 +161,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   } else {
     n0 = static_cast<int64_t>(blockIdx.y) * 128 + wave * 32;
     n1 = n0 + 16;
-    if (n0 >= p.out_width) return;
+    if (!kByExpert && n0 >= p.out_width) return;  // (expert-major FC2: whole 128-column slices)
   }
   // Line load i of a stage (i = 0..7): line i / 4 of rows 8 (i % 4) + l / 8 of the wave's 32 (set
   // 0 = rows n0.., set 1 = rows n1..), 16-byte chunk l % 8.
@@ -150,6 +175,69 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   const int source1 = source0 + 4;            // s odd
   const int stages = static_cast<int>(p.K / 128);
 
+  struct Stage {
+    u32x4 lines[8];
+    u32x4 act[kPassTiles][4];
+  };
+  auto load_lines = [&](Stage &st, int64_t k) {
+    const int64_t offset = k * 128;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int set = (i % 4) / 2;
+      const int64_t row_offset = static_cast<int64_t>((i % 4) % 2) * 8 * p.K;
+      st.lines[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(line_row[set] + row_offset + offset + (i / 4) * 64));
+    }
+  };
+  Stage even, odd;
+  if constexpr (kByExpert) load_lines(even, 0);  // no dependence on the routes: out before the scan
+
+  // Expert-major: the route list. Wavefront w ballots routes [w q, (w + 1) q) (q whole chunks of
+  // 64) into its own stretch of the list; the stretches, in wave order, are the routes in order.
+  __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
+  __shared__ int32_t wave_count[kWaves + 1];
+  const int64_t per_wave = ((p.routes + kScanChunk - 1) / kScanChunk + kWaves - 1) / kWaves * kScanChunk;
+  if constexpr (kByExpert) {
+    const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+    const int64_t begin = wave * per_wave;
+    const int64_t end = begin + per_wave < p.routes ? begin + per_wave : p.routes;
+    const int32_t want = static_cast<int32_t>(expert + p.local_offset);
+    int32_t *mine = route_list + wave * per_wave;
+    int count = 0;
+    for (int64_t c = begin; c < end; c += 4 * kScanChunk) {
+      int32_t id[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t route = c + u * kScanChunk + lane;
+        id[u] = route < end && route < live ? p.ids[route] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool match = id[u] == want;
+        const uint64_t mask = __ballot(match);
+        if (match) mine[count + __popcll(mask & ((1ull << lane) - 1))] = static_cast<int32_t>(c + u * kScanChunk + lane);
+        count += __popcll(mask);
+      }
+    }
+    if (lane == 0) wave_count[wave] = count;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int total = 0;
+      for (int w = 0; w < kWaves; ++w) total += wave_count[w];
+      wave_count[kWaves] = total;
+    }
+    __syncthreads();
+    rows = wave_count[kWaves];
+    if (rows == 0) return;
+  }
+  // The route of list row m (expert-major).
+  auto listed = [&](int m) -> int64_t {
+    int w = 0;
+    int before = 0;
+    while (w + 1 < kWaves && m >= before + wave_count[w]) before += wave_count[w++];
+    return route_list[w * per_wave + (m - before)];
+  };
+
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint16_t *a[kPassTiles];
     bool valid[kPassTiles];
@@ -158,7 +246,12 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
       const int m = pass + ms * 16 + r16;
       valid[ms] = m < rows;
       int64_t source = first + m;
-      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      if constexpr (kByExpert) {
+        source = valid[ms] ? listed(m) : 0;
+        if constexpr (kGated) source /= p.top;
+      } else if constexpr (kGated) {
+        source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      }
       a[ms] = p.act + (valid[ms] ? source : 0) * p.K + g * 8;
     }
     floatx4 acc[2][kPassTiles];
@@ -167,24 +260,17 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) acc[set][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    struct Stage {
-      u32x4 lines[8];
-      u32x4 act[kPassTiles][4];
-    };
-    auto load = [&](Stage &st, int64_t k) {
+    auto load_act = [&](Stage &st, int64_t k) {
       const int64_t offset = k * 128;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int set = (i % 4) / 2;
-        const int64_t row_offset = static_cast<int64_t>((i % 4) % 2) * 8 * p.K;
-        st.lines[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(line_row[set] + row_offset + offset + (i / 4) * 64));
-      }
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms)
 #pragma unroll
         for (int s = 0; s < 4; ++s)
           st.act[ms][s] = valid[ms] ? load16(a[ms] + offset + s * 32) : u32x4{0, 0, 0, 0};
+    };
+    auto load = [&](Stage &st, int64_t k) {
+      load_lines(st, k);
+      load_act(st, k);
     };
     auto compute = [&](const Stage &st) {
 #pragma unroll
@@ -201,8 +287,8 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
         }
       }
     };
-    Stage even, odd;
-    load(even, 0);
+    if (kByExpert && pass == 0) load_act(even, 0);  // its weight lines went out before the route scan
+    else load(even, 0);
     for (int k = 0; k < stages; k += 2) {
       if (k + 1 < stages) load(odd, k + 1);
       compute(even);
@@ -215,7 +301,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
     for (int ms = 0; ms < kPassTiles; ++ms) {
       const int m = pass + ms * 16 + r16;
       if (m >= rows) continue;
-      uint16_t *row = p.out + (first + m) * p.out_width;
+      uint16_t *row = p.out + (kByExpert ? listed(m) : first + m) * p.out_width;
       if constexpr (kGated) {
         floatx4 h;
 #pragma unroll
@@ -388,6 +474,34 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
 }  // namespace uniserve
 
 namespace uniserve {
+
+bool expert_stream_fits(int64_t routes, int64_t local_experts, int64_t K, int64_t out_width, bool gated) {
+  return routes >= 1 && routes <= kExpertRoutes && routes < kStreamRowsPerExpert * local_experts && K % 128 == 0 &&
+         (gated ? out_width % 64 == 0 : out_width % 128 == 0) && local_experts <= 0x7fffffffLL;
+}
+
+void launch_expert_stream(const ExpertStream &e, bool gated, hipStream_t stream) {
+  GroupedParams p{};
+  p.act = static_cast<const uint16_t *>(e.act);
+  p.weights = static_cast<const uint16_t *>(e.weights);
+  p.out = static_cast<uint16_t *>(e.out);
+  p.K = e.K;
+  p.n_total = e.n_total;
+  p.out_width = e.out_width;
+  p.top = e.top;
+  p.activation = e.activation;
+  p.ids = e.ids;
+  p.live_tokens = e.live_tokens;
+  p.routes = e.routes;
+  p.local_offset = e.local_offset;
+  const bool one_pass = e.routes <= kOnePassRowsPerExpert * e.local_experts;
+  const int64_t slices = gated ? e.out_width / 64 : e.out_width / 128;
+  const dim3 grid(static_cast<uint32_t>(e.local_experts), static_cast<uint32_t>(slices));
+  if (gated && one_pass) hipLaunchKernelGGL((stream_kernel<true, 1, true>), grid, dim3(kThreads), 0, stream, p);
+  else if (gated) hipLaunchKernelGGL((stream_kernel<true, 2, true>), grid, dim3(kThreads), 0, stream, p);
+  else if (one_pass) hipLaunchKernelGGL((stream_kernel<false, 1, true>), grid, dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((stream_kernel<false, 2, true>), grid, dim3(kThreads), 0, stream, p);
+}
 
 int32_t gather_gemm_bf16(const uniserve_gather_call *call, int32_t activation, void *stream) {
   return guarded(call, [&]() -> int32_t {

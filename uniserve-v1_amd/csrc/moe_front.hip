@@ -135,6 +135,19 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   }
   __syncthreads();
   UNISERVE_TRACE(2);
+  if (!p.sort_routes) {
+    // No sort: each route of the block is visible at its own expanded index, or not at all.
+    const int64_t live = (p.live != nullptr ? static_cast<int64_t>(p.live[0]) : p.tokens) * p.top;
+    const int64_t block_first = static_cast<int64_t>(blockIdx.x) * kTile * p.top;
+    for (int64_t i = threadIdx.x; i < kTile * p.top; i += kThreads) {
+      const int64_t route = block_first + i;
+      if (route >= p.tokens * p.top) break;
+      const int64_t local = static_cast<int64_t>(load_device(p.ids + route)) - p.sort.local_offset;
+      const bool visible = route < live && local >= 0 && local < p.sort.local_experts;
+      p.sort.expanded_to_permuted[route] = visible ? static_cast<int32_t>(route) : -1;
+    }
+    return;
+  }
 
   // 3. The last of the token blocks sorts every route.
   if (!last_ticket(p.ticket, gridDim.x, &flag)) return;

@@ -31,6 +31,10 @@ struct FrontParams {
   float *weights;           ///< [tokens, top]
   uint32_t *ticket;         ///< [1 + kFrontTokenBlocks] counters, zero before the launch and after it
   sort::SortParams sort;    ///< the sort over `ids` (its ids pointer is `ids`)
+  /// 0: no sort - the routing workgroups write sort.expanded_to_permuted as each route's own
+  /// expanded index where it is live and in the window, -1 elsewhere (for products that find their
+  /// routes themselves and keep rows at expanded positions), and nothing else of the sort's.
+  int32_t sort_routes;
 };
 
 /// Whether one launch serves these extents: the router's split-contraction tiles, a router of at

@@ -13,6 +13,7 @@
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_mx.hpp"
+#include "expert_stream.hpp"
 #include "moe_front.hpp"
 #include "router_gemm.hpp"
 #include "uniserve_gather_gemm.h"
@@ -250,6 +251,13 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (call->tokens == 0) return 0;
     if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
     const int32_t activation = static_cast<int32_t>(call->activation);
+    // bf16 at decode sizes: no sort - the fused front end routes, and the products' workgroups
+    // each serve one local expert, finding its routes in `ids` (rows at expanded positions).
+    const int64_t routes = call->tokens * call->top;
+    const bool front = front_fits(call->tokens, call->experts, call->hidden_size, call->top, local_experts);
+    const bool by_expert = front && !fp8 && !mx &&
+                           expert_stream_fits(routes, local_experts, call->hidden_size, call->intermediate, true) &&
+                           expert_stream_fits(routes, local_experts, call->intermediate, call->hidden_size, false);
 
     char *ws = static_cast<char *>(workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
@@ -266,7 +274,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
 
     // Decode sizes: router, topk and sort in one launch (at the ROUTER step; TOPK and SORT launch
     // nothing).
-    if (front_fits(call->tokens, call->experts, call->hidden_size, call->top, local_experts)) {
+    if (front) {
       if (want(UNISERVE_MOE_LAYER_ROUTER)) {
         FrontParams fp{};
         fp.x = static_cast<const uint16_t *>(call->hidden);
@@ -302,6 +310,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         int bits = 0;
         while ((1ll << bits) <= local_experts) ++bits;
         sp.key_bits = bits;
+        fp.sort_routes = by_expert ? 0 : 1;
         launch_front(fp, s);
         if (int32_t status = launched(call, "router, topk and sort")) return status;
       }
@@ -350,6 +359,37 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     // 4-5. The two products.
     if (mx) {
       if (int32_t status = run_mx_products(call, v, ws, want, stream)) return status;
+    } else if (by_expert) {
+      ExpertStream e{};
+      e.ids = ids;
+      e.live_tokens = call->live_tokens;
+      e.routes = routes;
+      e.top = call->top;
+      e.local_offset = call->local_offset;
+      e.local_experts = local_experts;
+      e.activation = activation;
+      if (want(UNISERVE_MOE_LAYER_GATHER)) {
+        ExpertStream fc1 = e;
+        fc1.act = call->hidden;
+        fc1.weights = call->up_gate;
+        fc1.out = at(v.gated);
+        fc1.K = call->hidden_size;
+        fc1.n_total = 2 * call->intermediate;
+        fc1.out_width = call->intermediate;
+        launch_expert_stream(fc1, true, s);
+        if (int32_t status = launched(call, "gather_gemm")) return status;
+      }
+      if (want(UNISERVE_MOE_LAYER_ROUTE)) {
+        ExpertStream fc2 = e;
+        fc2.act = at(v.gated);
+        fc2.weights = call->down;
+        fc2.out = at(v.products);
+        fc2.K = call->intermediate;
+        fc2.n_total = call->hidden_size;
+        fc2.out_width = call->hidden_size;
+        launch_expert_stream(fc2, false, s);
+        if (int32_t status = launched(call, "route_gemm")) return status;
+      }
     } else if (!fp8) {
       uniserve_gather_call fc1{};
       fc1.hidden = call->hidden;
@@ -469,7 +509,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       if (want(UNISERVE_MOE_LAYER_ROUTE) && route_gemm_fp8(&fc2, scale_rows, stream) != 0) return forward_error(call, "route_gemm_fp8", fc2);
     }
 
-    // 6. The weighted combine, permuted layout.
+    // 6. The weighted combine: permuted layout, or expanded where the products kept rows there.
     uniserve_unpermute_call combine{};
     combine.routes = at(v.products);
     combine.out = call->out;
@@ -482,7 +522,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     combine.input_dtype = UNISERVE_DTYPE_BF16;
     combine.scales_dtype = UNISERVE_DTYPE_F32;
     combine.output_dtype = UNISERVE_DTYPE_BF16;
-    combine.layout = UNISERVE_UNPERMUTE_LAYOUT_PERMUTED;
+    combine.layout = by_expert ? UNISERVE_UNPERMUTE_LAYOUT_EXPANDED : UNISERVE_UNPERMUTE_LAYOUT_PERMUTED;
     if (want(UNISERVE_MOE_LAYER_UNPERMUTE) && uniserve_moe_unpermute(&combine, stream) != 0) return forward_error(call, "moe_unpermute", combine);
     return 0;
   });
