@@ -38,6 +38,7 @@ ROUTED = {
     "bf16 decode, map + load + window + live": (64, 2048, 128, 8, 768, "bf16", (32, 48), 50),
     "bf16 prefill, map + load + window": (2048, 2048, 128, 8, 768, "bf16", (16, 96), None),
     "fp8 decode, map + load + window": (64, 2048, 128, 8, 768, "f8e4m3", (40, 64), None),
+    "fp8 decode, map + load + window + live": (64, 2048, 128, 8, 768, "f8e4m3", (40, 64), 50),
     "fp8 prefill, map + load + window + live": (2048, 2048, 128, 8, 768, "f8e4m3", (0, 100), 2000),
     "mx decode, map + load + window": (64, 2048, 128, 8, 768, "f4e2m1", (64, 64), None),
     "mx prefill, map + load + window": (2048, 2048, 128, 8, 768, "f4e2m1", (8, 112), None),

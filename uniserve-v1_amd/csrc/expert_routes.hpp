@@ -1,0 +1,69 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// The routes of one local expert, found by the workgroup that serves it (decode products without
+// a sort): the routes whose id is the expert's, in route order - the order the sort's stable
+// placement gives them.
+#pragma once
+
+#include "common.hpp"
+
+namespace uniserve {
+
+/// The most routes an expert-major workgroup lists (a decode batch's).
+constexpr int kExpertRoutes = 4096;
+
+/// Routes each wavefront of a kWaves-wave workgroup scans (whole chunks of 64).
+template <int kWaves>
+__host__ __device__ constexpr int64_t routes_per_wave(int64_t routes) {
+  return ((routes + kWave - 1) / kWave + kWaves - 1) / kWaves * kWave;
+}
+
+/// Lists the live routes (route < live) whose id is `want`: wavefront w ballots routes
+/// [w q, (w + 1) q), q = routes_per_wave, into list[w q ..] and counts[w]; counts[kWaves] is the
+/// total. Every thread of the workgroup calls it (two barriers); returns the total.
+template <int kWaves>
+__device__ __forceinline__ int list_expert_routes(const int32_t *ids, int64_t routes, int64_t live, int32_t want,
+                                                  int32_t *list, int32_t *counts) {
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int64_t per_wave = routes_per_wave<kWaves>(routes);
+  const int64_t begin = wave * per_wave;
+  const int64_t end = begin + per_wave < routes ? begin + per_wave : routes;
+  int32_t *mine = list + wave * per_wave;
+  int count = 0;
+  for (int64_t c = begin; c < end; c += 4 * kWave) {
+    int32_t id[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t route = c + u * kWave + lane;
+      id[u] = route < end && route < live ? ids[route] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool match = id[u] == want;
+      const uint64_t mask = __ballot(match);
+      if (match) mine[count + __popcll(mask & ((1ull << lane) - 1))] = static_cast<int32_t>(c + u * kWave + lane);
+      count += __popcll(mask);
+    }
+  }
+  if (lane == 0) counts[wave] = count;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int total = 0;
+    for (int w = 0; w < kWaves; ++w) total += counts[w];
+    counts[kWaves] = total;
+  }
+  __syncthreads();
+  return counts[kWaves];
+}
+
+/// Row m of the list (m < the total).
+template <int kWaves>
+__device__ __forceinline__ int64_t listed_route(const int32_t *list, const int32_t *counts, int64_t routes, int m) {
+  int w = 0;
+  int before = 0;
+  while (w + 1 < kWaves && m >= before + counts[w]) before += counts[w++];
+  return list[w * routes_per_wave<kWaves>(routes) + (m - before)];
+}
+
+}  // namespace uniserve

@@ -23,7 +23,8 @@ struct ExpertStream {
 };
 
 /// Whether the expert-major stream kernel serves these extents (decode batches: at most 4096
-/// routes, few per expert; FC1 widths of whole 64-column slices, FC2 of whole 128-column ones).
+/// routes, at least one and fewer than 24 per local expert; FC1 widths of whole 64-column slices,
+/// FC2 of whole 128-column ones).
 bool expert_stream_fits(int64_t routes, int64_t local_experts, int64_t K, int64_t out_width, bool gated);
 
 /// FC1 (`gated`: the gate of `activation` times the up half) or FC2 over the listed routes.

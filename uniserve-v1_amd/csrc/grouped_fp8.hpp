@@ -120,6 +120,12 @@ struct GroupedFp8Params {
   int64_t scale_rows;           ///< nonzero (prefill kernel only): act_scales and out_code_scales are
                                 ///< route-major, [blocks, scale_rows] by permuted row
   int32_t activation;           ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
+  // Expert-major stream (decode, no sort): workgroup x serves local expert x, whose rows are the
+  // routes naming it in `ids`, at their expanded positions (act rows: FC1 route / top, FC2 route).
+  const int32_t *ids;
+  const int32_t *live_tokens;
+  int64_t routes;
+  int64_t local_offset;
 };
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,
@@ -127,6 +133,8 @@ void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream);
 bool fp8_stream_path(int64_t routes, int64_t experts);
+/// The expert-major stream kernel over `local_experts` workgroup columns (p.ids .. set).
+void launch_expert_stream_fp8(const GroupedFp8Params &p, bool gated, int64_t local_experts, hipStream_t stream);
 
 /// The quantiser over token rows that also scatters each scale to the permuted rows of the
 /// token's routes: route_scales[g, expanded_to_permuted[t, k]] for every held route (k < top).

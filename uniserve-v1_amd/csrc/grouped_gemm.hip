@@ -34,6 +34,7 @@
 // FP32 summation order.
 #include "common.hpp"
 #include "grouped_pair.hpp"
+#include "expert_routes.hpp"
 #include "expert_stream.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_gather_gemm.h"
@@ -124,10 +125,6 @@ __device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
   do {                    \
   } while (0)
 #endif
-/// Most routes one expert-major workgroup serves (the routes of a decode batch).
-constexpr int kExpertRoutes = 4096;
-constexpr int kScanChunk = kWave;
-
 /// kByExpert: workgroup x serves local expert x (grid: local experts x slices) and finds its rows
 /// itself - the routes whose id is the expert's, in route order, live ones only (each wavefront
 /// ballots a quarter of the routes into a list in LDS) - while its first weight stage is in
@@ -192,51 +189,16 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   Stage even, odd;
   if constexpr (kByExpert) load_lines(even, 0);  // no dependence on the routes: out before the scan
 
-  // Expert-major: the route list. Wavefront w ballots routes [w q, (w + 1) q) (q whole chunks of
-  // 64) into its own stretch of the list; the stretches, in wave order, are the routes in order.
+  // Expert-major: the route list (route order), found while the first weight stage is in flight.
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t wave_count[kWaves + 1];
-  const int64_t per_wave = ((p.routes + kScanChunk - 1) / kScanChunk + kWaves - 1) / kWaves * kScanChunk;
   if constexpr (kByExpert) {
     const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
-    const int64_t begin = wave * per_wave;
-    const int64_t end = begin + per_wave < p.routes ? begin + per_wave : p.routes;
-    const int32_t want = static_cast<int32_t>(expert + p.local_offset);
-    int32_t *mine = route_list + wave * per_wave;
-    int count = 0;
-    for (int64_t c = begin; c < end; c += 4 * kScanChunk) {
-      int32_t id[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t route = c + u * kScanChunk + lane;
-        id[u] = route < end && route < live ? p.ids[route] : -1;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const bool match = id[u] == want;
-        const uint64_t mask = __ballot(match);
-        if (match) mine[count + __popcll(mask & ((1ull << lane) - 1))] = static_cast<int32_t>(c + u * kScanChunk + lane);
-        count += __popcll(mask);
-      }
-    }
-    if (lane == 0) wave_count[wave] = count;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int total = 0;
-      for (int w = 0; w < kWaves; ++w) total += wave_count[w];
-      wave_count[kWaves] = total;
-    }
-    __syncthreads();
-    rows = wave_count[kWaves];
+    rows = list_expert_routes<kWaves>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
+                                      route_list, wave_count);
     if (rows == 0) return;
   }
-  // The route of list row m (expert-major).
-  auto listed = [&](int m) -> int64_t {
-    int w = 0;
-    int before = 0;
-    while (w + 1 < kWaves && m >= before + wave_count[w]) before += wave_count[w++];
-    return route_list[w * per_wave + (m - before)];
-  };
+  auto listed = [&](int m) -> int64_t { return listed_route<kWaves>(route_list, wave_count, p.routes, m); };
 
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint16_t *a[kPassTiles];
@@ -476,7 +438,10 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
 namespace uniserve {
 
 bool expert_stream_fits(int64_t routes, int64_t local_experts, int64_t K, int64_t out_width, bool gated) {
-  return routes >= 1 && routes <= kExpertRoutes && routes < kStreamRowsPerExpert * local_experts && K % 128 == 0 &&
+  // At least one route per local expert on average: with fewer, most of the grid's workgroups
+  // would find no route (one token: 8 of 128 experts) and only delay the ones that do.
+  return routes >= local_experts && routes <= kExpertRoutes && routes < kStreamRowsPerExpert * local_experts &&
+         K % 128 == 0 &&
          (gated ? out_width % 64 == 0 : out_width % 128 == 0) && local_experts <= 0x7fffffffLL;
 }
 

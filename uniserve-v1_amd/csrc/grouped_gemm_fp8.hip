@@ -17,6 +17,7 @@
 #include "grouped_fp8.hpp"
 #include "grouped_dual.hpp"
 #include "grouped_pair.hpp"
+#include "expert_routes.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_moe_fp8.h"
 
@@ -121,14 +122,32 @@ constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is spli
 /// meeting in LDS in wave order - four times the workgroups, for batches whose tiles x slices would
 /// leave most of the chip idle (a single token: 8 tiles).
 /// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
-template <bool kGated, bool kSplit, int kPassTiles>
+/// kByExpert: workgroup x serves local expert x and lists its rows itself (the routes naming it in
+/// `ids`, route order), reading act row route / top (FC1) or route (FC2) and writing row `route`.
+template <bool kGated, bool kSplit, int kPassTiles, bool kByExpert = false>
 __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p) {
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
-  const int tile = static_cast<int>(blockIdx.x);
-  if (tile >= p.num_tiles[0]) return;
-  const int64_t expert = p.tile_to_expert[tile];
-  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
-  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
+  __shared__ int32_t route_count[kThreads / kWave + 1];
+  int64_t expert, first;
+  int rows;
+  if constexpr (kByExpert) {
+    expert = blockIdx.x;
+    first = 0;
+    const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+    rows = list_expert_routes<kThreads / kWave>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
+                                                route_list, route_count);
+    if (rows == 0) return;
+  } else {
+    const int tile = static_cast<int>(blockIdx.x);
+    if (tile >= p.num_tiles[0]) return;
+    expert = p.tile_to_expert[tile];
+    first = static_cast<int64_t>(tile) * kTileRows;
+    rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  }
+  auto listed = [&](int m) -> int64_t {
+    return listed_route<kThreads / kWave>(route_list, route_count, p.routes, m);
+  };
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int r16 = lane & 15;
@@ -143,7 +162,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   } else {
     n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
     n1 = n0 + 16;
-    if (n0 >= p.out_width) return;
+    if (n0 >= p.out_width) return;  // (expert-major: whole slices, so no wave leaves here)
   }
   const int64_t kb_first = kSplit ? wave : 0;
   const int64_t kb_step = kSplit ? kThreads / kWave : 1;
@@ -170,7 +189,12 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
       const int m = pass + ms * 16 + r16;
       valid[ms] = m < rows;
       int64_t source = first + m;
-      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      if constexpr (kByExpert) {
+        source = valid[ms] ? listed(m) : 0;
+        if constexpr (kGated) source /= p.top;
+      } else if constexpr (kGated) {
+        source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      }
       if (!valid[ms]) source = 0;
       a[ms] = p.act + source * p.K + g * 16;
       as[ms] = p.act_scales + source * kb_count;
@@ -320,7 +344,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     for (int ms = 0; ms < kPassTiles; ++ms) {
       const int m = pass + ms * 16 + r16;
       if (m >= rows) continue;
-      uint16_t *row = p.out + (first + m) * p.out_width;
+      uint16_t *row = p.out + (kByExpert ? listed(m) : first + m) * p.out_width;
       if constexpr (kGated) {
         floatx4 h;
 #pragma unroll
@@ -576,6 +600,26 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
 }
 
 bool fp8_stream_path(int64_t routes, int64_t experts) { return routes < kStreamRowsPerExpert * experts; }
+
+void launch_expert_stream_fp8(const GroupedFp8Params &p, bool gated, int64_t local_experts, hipStream_t stream) {
+  const bool one_pass = p.routes <= kOnePassRowsPerExpert * local_experts;
+  const int64_t slices = gated ? p.out_width / 64 : p.out_width / 128;
+  // Workgroups with routes: at most one per route.
+  const int64_t served = p.routes < local_experts ? p.routes : local_experts;
+  if (served * slices < kSplitBelow) {
+    const dim3 grid(static_cast<uint32_t>(local_experts), static_cast<uint32_t>(gated ? p.out_width / 16 : p.out_width / 32));
+    if (gated && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
+    else if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
+    else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
+    return;
+  }
+  const dim3 grid(static_cast<uint32_t>(local_experts), static_cast<uint32_t>(slices));
+  if (gated && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, false, 1, true>), grid, dim3(kThreads), 0, stream, p);
+  else if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, false, 2, true>), grid, dim3(kThreads), 0, stream, p);
+  else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, false, 1, true>), grid, dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((stream_fp8_kernel<false, false, 2, true>), grid, dim3(kThreads), 0, stream, p);
+}
 
 }  // namespace uniserve
 

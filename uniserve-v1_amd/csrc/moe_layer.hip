@@ -251,11 +251,12 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (call->tokens == 0) return 0;
     if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
     const int32_t activation = static_cast<int32_t>(call->activation);
-    // bf16 at decode sizes: no sort - the fused front end routes, and the products' workgroups
-    // each serve one local expert, finding its routes in `ids` (rows at expanded positions).
+    // bf16 and e4m3 at decode sizes: no sort - the fused front end routes, and the products'
+    // workgroups each serve one local expert, finding its routes in `ids` (rows at expanded
+    // positions).
     const int64_t routes = call->tokens * call->top;
     const bool front = front_fits(call->tokens, call->experts, call->hidden_size, call->top, local_experts);
-    const bool by_expert = front && !fp8 && !mx &&
+    const bool by_expert = front && !mx &&
                            expert_stream_fits(routes, local_experts, call->hidden_size, call->intermediate, true) &&
                            expert_stream_fits(routes, local_experts, call->intermediate, call->hidden_size, false);
 
@@ -359,7 +360,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     // 4-5. The two products.
     if (mx) {
       if (int32_t status = run_mx_products(call, v, ws, want, stream)) return status;
-    } else if (by_expert) {
+    } else if (by_expert && !fp8) {
       ExpertStream e{};
       e.ids = ids;
       e.live_tokens = call->live_tokens;
@@ -446,6 +447,48 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         return forward_error(call, "quantize_fp8", qx);
       }
 
+      if (by_expert) {
+        // Decode: expert-major products over rows at expanded positions; the gated quantiser
+        // takes every route's row (rows of routes not served are never read).
+        GroupedFp8Params e{};
+        e.ids = ids;
+        e.live_tokens = call->live_tokens;
+        e.routes = routes;
+        e.local_offset = call->local_offset;
+        e.top = call->top;
+        e.activation = activation;
+        if (want(UNISERVE_MOE_LAYER_GATHER)) {
+          GroupedFp8Params fc1 = e;
+          fc1.act = static_cast<const uint8_t *>(at(v.hidden_q));
+          fc1.act_scales = static_cast<const float *>(at(v.hidden_s));
+          fc1.weights = static_cast<const uint8_t *>(call->up_gate);
+          fc1.weight_scales = call->up_gate_scales;
+          fc1.out = static_cast<uint16_t *>(at(v.gated));
+          fc1.K = call->hidden_size;
+          fc1.n_total = 2 * call->intermediate;
+          fc1.out_width = call->intermediate;
+          launch_expert_stream_fp8(fc1, true, local_experts, s);
+          if (int32_t status = launched(call, "gather_gemm_fp8")) return status;
+        }
+        if (want(UNISERVE_MOE_LAYER_QUANTIZE_GATED)) {
+          launch_quantize_fp8(at(v.gated), false, static_cast<uint8_t *>(at(v.gated_q)), static_cast<float *>(at(v.gated_s)),
+                              nullptr, routes, call->intermediate, s);
+          if (int32_t status = launched(call, "quantize_fp8")) return status;
+        }
+        if (want(UNISERVE_MOE_LAYER_ROUTE)) {
+          GroupedFp8Params fc2 = e;
+          fc2.act = static_cast<const uint8_t *>(at(v.gated_q));
+          fc2.act_scales = static_cast<const float *>(at(v.gated_s));
+          fc2.weights = static_cast<const uint8_t *>(call->down);
+          fc2.weight_scales = call->down_scales;
+          fc2.out = static_cast<uint16_t *>(at(v.products));
+          fc2.K = call->intermediate;
+          fc2.n_total = call->hidden_size;
+          fc2.out_width = call->hidden_size;
+          launch_expert_stream_fp8(fc2, false, local_experts, s);
+          if (int32_t status = launched(call, "route_gemm_fp8")) return status;
+        }
+      } else {
       uniserve_gather_fp8_call fc1{};
       fc1.hidden = at(v.hidden_q);
       fc1.hidden_scales = static_cast<const float *>(at(scale_rows != 0 ? v.hidden_route_s : v.hidden_s));
@@ -507,6 +550,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       fc2.out_dtype = UNISERVE_DTYPE_BF16;
       fc2.multiprocessors = call->multiprocessors;
       if (want(UNISERVE_MOE_LAYER_ROUTE) && route_gemm_fp8(&fc2, scale_rows, stream) != 0) return forward_error(call, "route_gemm_fp8", fc2);
+      }
     }
 
     // 6. The weighted combine: permuted layout, or expanded where the products kept rows there.
