@@ -130,14 +130,10 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t route_count[kThreads / kWave + 1];
   int64_t expert, first;
-  int rows;
+  int rows = 0;
   if constexpr (kByExpert) {
     expert = blockIdx.x;
     first = 0;
-    const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
-    rows = list_expert_routes<kThreads / kWave>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
-                                                route_list, route_count);
-    if (rows == 0) return;
   } else {
     const int tile = static_cast<int>(blockIdx.x);
     if (tile >= p.num_tiles[0]) return;
@@ -162,7 +158,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   } else {
     n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
     n1 = n0 + 16;
-    if (n0 >= p.out_width) return;  // (expert-major: whole slices, so no wave leaves here)
+    if (!kByExpert && n0 >= p.out_width) return;  // (expert-major: whole slices only)
   }
   const int64_t kb_first = kSplit ? wave : 0;
   const int64_t kb_step = kSplit ? kThreads / kWave : 1;
@@ -179,6 +175,22 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   const int source_hi = source_lo + 4;      // chunk g + 4
   const float *ws0 = p.weight_scales + (expert * (p.n_total / 128) + n0 / 128) * kb_count;
   const float *ws1 = p.weight_scales + (expert * (p.n_total / 128) + n1 / 128) * kb_count;
+
+  // Expert-major: the first weight block goes out before the route scan (it depends on nothing the
+  // routes decide), then the scan lists the expert's rows.
+  u32x4 wcur[4], wnext[4];  // the unsplit form's weight lines of alternate blocks
+  if constexpr (kByExpert && !kSplit) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      wcur[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * p.K + kb_first * 128));
+  }
+  if constexpr (kByExpert) {
+    const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+    rows = list_expert_routes<kThreads / kWave>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
+                                                route_list, route_count);
+    if (rows == 0) return;
+  }
 
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint8_t *a[kPassTiles];
@@ -205,11 +217,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto fetch = [&](int64_t kb, u32x4 (&w)[4], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * p.K + kb * 128));
+    auto fetch_rest = [&](int64_t kb, intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
       s[0] = ws0[kb];
       s[1] = ws1[kb];
 #pragma unroll
@@ -224,6 +232,13 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
         }
         s[2 + ms] = valid[ms] ? as[ms][kb] : 0.0f;
       }
+    };
+    auto fetch = [&](int64_t kb, u32x4 (&w)[4], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * p.K + kb * 128));
+      fetch_rest(kb, x, s);
     };
     auto compute = [&](const u32x4 (&lines)[4], const intx8 (&x)[kPassTiles], const float (&s)[2 + kPassTiles]) {
       intx8 w[2];
@@ -308,10 +323,13 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
         }
       }
     } else {
-    u32x4 wcur[4], wnext[4];
     intx8 acur[kPassTiles], anext[kPassTiles];
     float scur[2 + kPassTiles], snext[2 + kPassTiles];
-    if (kb_first < kb_count) fetch(kb_first, wcur, acur, scur);
+    if (kByExpert && pass == 0) {
+      fetch_rest(kb_first, acur, scur);  // its weight lines went out before the route scan
+    } else if (kb_first < kb_count) {
+      fetch(kb_first, wcur, acur, scur);
+    }
     for (int64_t kb = kb_first; kb < kb_count; kb += 2 * kb_step) {
       if (kb + kb_step < kb_count) fetch(kb + kb_step, wnext, anext, snext);
       compute(wcur, acur, scur);
