@@ -57,6 +57,38 @@ __device__ __forceinline__ int list_expert_routes(const int32_t *ids, int64_t ro
   return counts[kWaves];
 }
 
+/// Local experts a compact grid can tell apart (the fused front end's window bound).
+constexpr int kPresentExperts = 512;
+
+/// The n-th smallest local expert that some live route names, or -1 when fewer are named: the
+/// workgroup marks the named experts in an LDS bitmap (`bits`, kPresentExperts / 32 words) and
+/// every thread counts its way to the n-th mark. Every thread of the workgroup calls it (two
+/// barriers) and gets the same answer.
+template <int kThreads>
+__device__ __forceinline__ int32_t nth_named_expert(const int32_t *ids, int64_t routes, int64_t live, int32_t local_offset,
+                                                    int32_t local_experts, int n, uint32_t *bits) {
+  constexpr int kWords = kPresentExperts / 32;
+  if (threadIdx.x < kWords) bits[threadIdx.x] = 0u;
+  __syncthreads();
+  const int64_t last = routes < live ? routes : live;
+  for (int64_t route = threadIdx.x; route < last; route += kThreads) {
+    const int32_t local = ids[route] - local_offset;
+    if (local >= 0 && local < local_experts) atomicOr(bits + local / 32, 1u << (local % 32));
+  }
+  __syncthreads();
+  for (int w = 0; w < kWords; ++w) {
+    uint32_t word = bits[w];
+    const int count = __popc(word);
+    if (n >= count) {
+      n -= count;
+      continue;
+    }
+    for (; n > 0; --n) word &= word - 1;  // drop the n lowest marks
+    return 32 * w + __ffs(static_cast<int>(word)) - 1;
+  }
+  return -1;
+}
+
 /// Row m of the list (m < the total).
 template <int kWaves>
 __device__ __forceinline__ int64_t listed_route(const int32_t *list, const int32_t *counts, int64_t routes, int m) {

@@ -126,6 +126,8 @@ struct GroupedFp8Params {
   const int32_t *live_tokens;
   int64_t routes;
   int64_t local_offset;
+  int64_t local_experts;
+  int32_t compact;              ///< workgroup x serves the x-th named local expert
 };
 
 void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float *scales,

@@ -66,6 +66,8 @@ struct GroupedParams {
   const int32_t *live_tokens;
   int64_t routes;
   int64_t local_offset;
+  int64_t local_experts;
+  int32_t compact;          ///< workgroup x serves the x-th named local expert (fewer routes than experts)
 };
 
 __device__ __forceinline__ u32x4 load16(const uint16_t *pointer) {
@@ -139,9 +141,16 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   int64_t expert, first;
   int rows;
   if constexpr (kByExpert) {
-    expert = blockIdx.x;
     first = 0;
     rows = 0;
+    expert = blockIdx.x;
+    if (p.compact) {
+      __shared__ uint32_t named[kPresentExperts / 32];
+      const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+      expert = nth_named_expert<kThreads>(p.ids, p.routes, live, static_cast<int32_t>(p.local_offset),
+                                          static_cast<int32_t>(p.local_experts), static_cast<int>(blockIdx.x), named);
+      if (expert < 0) return;
+    }
   } else {
     const int tile = static_cast<int>(blockIdx.x);
     if (tile >= p.num_tiles[0]) return;
@@ -438,10 +447,10 @@ void launch_grouped(const GroupedParams &p, int64_t max_tiles, bool stream_path,
 namespace uniserve {
 
 bool expert_stream_fits(int64_t routes, int64_t local_experts, int64_t K, int64_t out_width, bool gated) {
-  // At least one route per local expert on average: with fewer, most of the grid's workgroups
-  // would find no route (one token: 8 of 128 experts) and only delay the ones that do.
-  return routes >= local_experts && routes <= kExpertRoutes && routes < kStreamRowsPerExpert * local_experts &&
-         K % 128 == 0 &&
+  // Fewer routes than local experts: a compact grid (a workgroup column per route, each finding
+  // the n-th named expert), which tells at most kPresentExperts experts apart.
+  return routes >= 1 && routes <= kExpertRoutes && routes < kStreamRowsPerExpert * local_experts &&
+         (routes >= local_experts || local_experts <= kPresentExperts) && K % 128 == 0 &&
          (gated ? out_width % 64 == 0 : out_width % 128 == 0) && local_experts <= 0x7fffffffLL;
 }
 
@@ -459,9 +468,11 @@ void launch_expert_stream(const ExpertStream &e, bool gated, hipStream_t stream)
   p.live_tokens = e.live_tokens;
   p.routes = e.routes;
   p.local_offset = e.local_offset;
+  p.local_experts = e.local_experts;
+  p.compact = e.routes < e.local_experts ? 1 : 0;
   const bool one_pass = e.routes <= kOnePassRowsPerExpert * e.local_experts;
   const int64_t slices = gated ? e.out_width / 64 : e.out_width / 128;
-  const dim3 grid(static_cast<uint32_t>(e.local_experts), static_cast<uint32_t>(slices));
+  const dim3 grid(static_cast<uint32_t>(p.compact ? e.routes : e.local_experts), static_cast<uint32_t>(slices));
   if (gated && one_pass) hipLaunchKernelGGL((stream_kernel<true, 1, true>), grid, dim3(kThreads), 0, stream, p);
   else if (gated) hipLaunchKernelGGL((stream_kernel<true, 2, true>), grid, dim3(kThreads), 0, stream, p);
   else if (one_pass) hipLaunchKernelGGL((stream_kernel<false, 1, true>), grid, dim3(kThreads), 0, stream, p);

@@ -134,6 +134,13 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   if constexpr (kByExpert) {
     expert = blockIdx.x;
     first = 0;
+    if (p.compact) {
+      __shared__ uint32_t named[kPresentExperts / 32];
+      const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+      expert = nth_named_expert<kThreads>(p.ids, p.routes, live, static_cast<int32_t>(p.local_offset),
+                                          static_cast<int32_t>(p.local_experts), static_cast<int>(blockIdx.x), named);
+      if (expert < 0) return;
+    }
   } else {
     const int tile = static_cast<int>(blockIdx.x);
     if (tile >= p.num_tiles[0]) return;
@@ -619,20 +626,24 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
 
 bool fp8_stream_path(int64_t routes, int64_t experts) { return routes < kStreamRowsPerExpert * experts; }
 
-void launch_expert_stream_fp8(const GroupedFp8Params &p, bool gated, int64_t local_experts, hipStream_t stream) {
+void launch_expert_stream_fp8(const GroupedFp8Params &params, bool gated, int64_t local_experts, hipStream_t stream) {
+  GroupedFp8Params p = params;
+  p.local_experts = local_experts;
+  p.compact = p.routes < local_experts ? 1 : 0;
+  const int64_t columns = p.compact ? p.routes : local_experts;  // workgroup columns
   const bool one_pass = p.routes <= kOnePassRowsPerExpert * local_experts;
   const int64_t slices = gated ? p.out_width / 64 : p.out_width / 128;
   // Workgroups with routes: at most one per route.
   const int64_t served = p.routes < local_experts ? p.routes : local_experts;
   if (served * slices < kSplitBelow) {
-    const dim3 grid(static_cast<uint32_t>(local_experts), static_cast<uint32_t>(gated ? p.out_width / 16 : p.out_width / 32));
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(gated ? p.out_width / 16 : p.out_width / 32));
     if (gated && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
     else if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
     else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
     return;
   }
-  const dim3 grid(static_cast<uint32_t>(local_experts), static_cast<uint32_t>(slices));
+  const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
   if (gated && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, false, 1, true>), grid, dim3(kThreads), 0, stream, p);
   else if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, false, 2, true>), grid, dim3(kThreads), 0, stream, p);
   else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, false, 1, true>), grid, dim3(kThreads), 0, stream, p);
