@@ -9,6 +9,8 @@
 
 #include <cstdint>
 
+#include "uniserve_moe_mx.h"
+
 namespace uniserve {
 
 struct ExpertStream {
@@ -22,12 +24,23 @@ struct ExpertStream {
   int32_t activation;        ///< FC1's gate
 };
 
-/// Whether the expert-major stream kernel serves these extents (decode batches: at most 4096
-/// routes, at least one and fewer than 24 per local expert; FC1 widths of whole 64-column slices,
-/// FC2 of whole 128-column ones).
+/// Whether the expert-major stream kernels serve these extents (decode batches: at most 4096
+/// routes, fewer than 24 per local expert - with fewer routes than local experts a compact grid over
+/// at most 512 of them; FC1 widths of whole 64-column slices, FC2 of whole 128-column ones).
 bool expert_stream_fits(int64_t routes, int64_t local_experts, int64_t K, int64_t out_width, bool gated);
 
 /// FC1 (`gated`: the gate of `activation` times the up half) or FC2 over the listed routes.
 void launch_expert_stream(const ExpertStream &e, bool gated, hipStream_t stream);
+
+/// The routes the expert-major MXFP4 products serve (their calls' tile maps are not read).
+struct ExpertRouting {
+  const int32_t *ids;
+  const int32_t *live_tokens;
+  int64_t routes, top, local_offset, local_experts;
+};
+
+void gather_gemm_mx_by_expert(const uniserve_gather_mx_call *call, const ExpertRouting &r, int32_t activation,
+                              void *stream);
+void route_gemm_mx_by_expert(const uniserve_route_mx_call *call, const ExpertRouting &r, void *stream);
 
 }  // namespace uniserve

@@ -23,6 +23,8 @@
 //    stages of 128 K.
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "expert_routes.hpp"
+#include "expert_stream.hpp"
 #include "grouped_mx.hpp"
 #include "grouped_prefill.hpp"
 #include "uniserve_moe_mx.h"
@@ -143,6 +145,14 @@ struct MxParams {
   int64_t as_row;
   int32_t as_by_route;           ///< activation scale rows are permuted rows, not act rows
   int32_t activation;            ///< FC1's gate: UNISERVE_ACTIVATION_SILU or _GELU_TANH
+  // Expert-major stream (decode, no sort): workgroup x serves local expert x (or, compact, the
+  // x-th named one), whose rows are the routes naming it in `ids`, at their expanded positions.
+  const int32_t *ids;
+  const int32_t *live_tokens;
+  int64_t routes;
+  int64_t local_offset;
+  int64_t local_experts;
+  int32_t compact;
 };
 
 /// Stride words of a scale table with `rows` rows in `layout`.
@@ -186,14 +196,36 @@ __device__ __forceinline__ floatx4 mfma_mx(const u32x4 &a, const intx8 &b, uint3
 /// chunks: one 128-byte line of each weight row, i.e. two 16x16x128 MFMAs per set (h = 0, 1).
 /// kSplit: the four waves share one row set and split the chunks (chunk c to wave c % 4), their
 /// partial sums meeting in LDS in wave order - for batches too small to fill the chip otherwise.
-template <bool kGated, bool kSplit>
+/// kByExpert: the rows are the routes naming the workgroup's local expert (FC1 reads token route /
+/// top, FC2 row `route`; both write row `route`), listed by the workgroup while its first weight
+/// chunk is in flight.
+template <bool kGated, bool kSplit, bool kByExpert = false>
 __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
-  const int tile = static_cast<int>(blockIdx.x);
-  if (tile >= p.num_tiles[0]) return;
-  const int64_t expert = p.tile_to_expert[tile];
-  const int64_t first = static_cast<int64_t>(tile) * kTileRows;
-  const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
+  __shared__ int32_t route_count[kThreads / kWave + 1];
+  int64_t expert, first;
+  int rows = 0;
+  if constexpr (kByExpert) {
+    expert = blockIdx.x;
+    first = 0;
+    if (p.compact) {
+      __shared__ uint32_t named[kPresentExperts / 32];
+      const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+      expert = nth_named_expert<kThreads>(p.ids, p.routes, live, static_cast<int32_t>(p.local_offset),
+                                          static_cast<int32_t>(p.local_experts), static_cast<int>(blockIdx.x), named);
+      if (expert < 0) return;
+    }
+  } else {
+    const int tile = static_cast<int>(blockIdx.x);
+    if (tile >= p.num_tiles[0]) return;
+    expert = p.tile_to_expert[tile];
+    first = static_cast<int64_t>(tile) * kTileRows;
+    rows = p.tile_to_limit[tile] - static_cast<int>(first);
+  }
+  auto listed = [&](int m) -> int64_t {
+    return listed_route<kThreads / kWave>(route_list, route_count, p.routes, m);
+  };
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int r16 = lane & 15;
@@ -210,7 +242,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   } else {
     n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
     n1 = n0 + 16;
-    if (n0 >= p.out_width) return;
+    if (!kByExpert && n0 >= p.out_width) return;  // (expert-major: whole slices only)
   }
   const int64_t c_first = kSplit ? wave : 0;
   const int64_t c_step = kSplit ? kThreads / kWave : 1;
@@ -228,6 +260,30 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   ws[0] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n0 + r16) * p.ws_row;
   ws[1] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n1 + r16) * p.ws_row;
 
+  // One chunk's operands: four weight lines, two 8-byte weight-scale words, and per token block
+  // 64 activation bytes (two MFMAs' worth: pieces g and g + 4 of each 128-byte half) and an
+  // 8-byte activation-scale word.
+  struct Chunk {
+    u32x4 lines[4];
+    uint2 wscale[2];
+    intx8 x[kPassTiles][2];
+    uint2 xscale[kPassTiles];
+  };
+  auto fetch_lines = [&](int64_t c, Chunk &d) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      d.lines[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * weight_row_bytes + c * 128));
+  };
+  Chunk cur, next;
+  if constexpr (kByExpert) {
+    if (!kSplit) fetch_lines(c_first, cur);  // it depends on nothing the routes decide
+    const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+    rows = list_expert_routes<kThreads / kWave>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
+                                                route_list, route_count);
+    if (rows == 0) return;
+  }
+
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint8_t *a[kPassTiles];
     const uint8_t *as[kPassTiles];
@@ -237,7 +293,12 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
       const int m = pass + ms * 16 + r16;
       valid[ms] = m < rows;
       int64_t source = first + m;
-      if constexpr (kGated) source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      if constexpr (kByExpert) {
+        source = valid[ms] ? listed(m) : 0;
+        if constexpr (kGated) source /= p.top;
+      } else if constexpr (kGated) {
+        source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
+      }
       if (!valid[ms]) source = 0;
       a[ms] = p.act + source * p.K + g * 16;
       as[ms] = p.act_scales + (p.as_by_route ? first + (valid[ms] ? m : 0) : source) * p.as_row;
@@ -248,20 +309,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) acc[s][ms] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // One chunk's operands: four weight lines, two 8-byte weight-scale words, and per token block
-    // 64 activation bytes (two MFMAs' worth: pieces g and g + 4 of each 128-byte half) and an
-    // 8-byte activation-scale word.
-    struct Chunk {
-      u32x4 lines[4];
-      uint2 wscale[2];
-      intx8 x[kPassTiles][2];
-      uint2 xscale[kPassTiles];
-    };
-    auto fetch = [&](int64_t c, Chunk &d) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        d.lines[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * weight_row_bytes + c * 128));
+    auto fetch_rest = [&](int64_t c, Chunk &d) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)
         d.wscale[s] = uint2{*reinterpret_cast<const uint32_t *>(ws[s] + 2 * c * p.ws_stage),
@@ -284,6 +332,10 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
                                  : uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
       }
     };
+    auto fetch = [&](int64_t c, Chunk &d) {
+      fetch_lines(c, d);
+      fetch_rest(c, d);
+    };
     // Byte 4 h + g of an 8-byte scale word: this lane's block of MFMA h.
     auto scale_byte = [&](const uint2 &word, int h) -> uint32_t { return ((h == 0 ? word.x : word.y) >> (8 * g)) & 0xffu; };
     auto compute = [&](const Chunk &d) {
@@ -303,8 +355,8 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
         }
       }
     };
-    Chunk cur, next;
-    if (c_first < chunks) fetch(c_first, cur);
+    if (kByExpert && !kSplit && pass == 0) fetch_rest(c_first, cur);  // its lines went out before the scan
+    else if (c_first < chunks) fetch(c_first, cur);
     for (int64_t c = c_first; c < chunks; c += 2 * c_step) {
       if (c + c_step < chunks) fetch(c + c_step, next);
       compute(cur);
@@ -336,7 +388,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     for (int ms = 0; ms < kPassTiles; ++ms) {
       const int m = pass + ms * 16 + r16;
       if (m >= rows) continue;
-      uint16_t *row = p.out + (first + m) * p.out_width;
+      uint16_t *row = p.out + (kByExpert ? listed(m) : first + m) * p.out_width;
       if constexpr (kGated) {
         floatx4 v;
 #pragma unroll
@@ -783,6 +835,65 @@ int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, vo
       launch_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
     return launched(call, "route_gemm_mx");
   });
+}
+
+namespace {
+
+void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_t stream) {
+  p.ids = r.ids;
+  p.live_tokens = r.live_tokens;
+  p.routes = r.routes;
+  p.local_offset = r.local_offset;
+  p.local_experts = r.local_experts;
+  p.compact = r.routes < r.local_experts ? 1 : 0;
+  const int64_t columns = p.compact ? r.routes : r.local_experts;
+  const int64_t slices = gated ? p.out_width / 64 : p.out_width / 128;
+  const int64_t served = r.routes < r.local_experts ? r.routes : r.local_experts;
+  if (served * slices < kSplitBelow) {
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(gated ? p.out_width / 16 : p.out_width / 32));
+    if (gated) hipLaunchKernelGGL((stream_mx_kernel<true, true, true>), grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((stream_mx_kernel<false, true, true>), grid, dim3(kThreads), 0, stream, p);
+    return;
+  }
+  const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
+  if (gated) hipLaunchKernelGGL((stream_mx_kernel<true, false, true>), grid, dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((stream_mx_kernel<false, false, true>), grid, dim3(kThreads), 0, stream, p);
+}
+
+}  // namespace
+
+void gather_gemm_mx_by_expert(const uniserve_gather_mx_call *call, const ExpertRouting &r, int32_t activation,
+                              void *stream) {
+  MxParams p{};
+  p.act = static_cast<const uint8_t *>(call->hidden);
+  p.act_scales = call->hidden_scales;
+  p.weights = static_cast<const uint8_t *>(call->weights);
+  p.weight_scales = call->weight_scales;
+  p.out = static_cast<uint16_t *>(call->out);
+  p.K = call->hidden_size;
+  p.n_total = call->width;
+  p.out_width = call->width / 2;
+  p.top = call->top;
+  p.activation = activation;
+  scale_strides(call->weight_scale_layout, p.n_total, p.K, &p.ws_stage, &p.ws_row);
+  scale_strides(UNISERVE_MX_SCALES_ROW_MAJOR, 0, p.K, &p.as_stage, &p.as_row);
+  launch_expert_mx(p, true, r, static_cast<hipStream_t>(stream));
+}
+
+void route_gemm_mx_by_expert(const uniserve_route_mx_call *call, const ExpertRouting &r, void *stream) {
+  MxParams p{};
+  p.act = static_cast<const uint8_t *>(call->rows);
+  p.act_scales = call->row_scales;
+  p.weights = static_cast<const uint8_t *>(call->weights);
+  p.weight_scales = call->weight_scales;
+  p.out = static_cast<uint16_t *>(call->out);
+  p.K = call->intermediate;
+  p.n_total = call->width;
+  p.out_width = call->width;
+  p.top = r.top;
+  scale_strides(call->weight_scale_layout, p.n_total, p.K, &p.ws_stage, &p.ws_row);
+  scale_strides(UNISERVE_MX_SCALES_ROW_MAJOR, 0, p.K, &p.as_stage, &p.as_row);
+  launch_expert_mx(p, false, r, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace uniserve

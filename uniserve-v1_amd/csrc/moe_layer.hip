@@ -116,9 +116,10 @@ extern "C" int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_s
 namespace {
 
 /// MXFP4 experts: quantise the hidden rows to MXFP8, FC1, quantise the live gated rows, FC2.
+/// `by_expert` set: the decode products without a sort (rows at expanded positions).
 template <class Want>
 int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_layer_views &v, char *ws,
-                        const Want &want, void *stream) {
+                        const Want &want, void *stream, const uniserve::ExpertRouting *by_expert) {
   using namespace uniserve;
   auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
   const auto *t2e = static_cast<const int32_t *>(at(v.tile_to_expert));
@@ -166,15 +167,21 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   fc1.out_dtype = UNISERVE_DTYPE_BF16;
   fc1.multiprocessors = call->multiprocessors;
   fc1.weight_scale_layout = call->weight_scale_layout;
-  if (want(UNISERVE_MOE_LAYER_GATHER) && gather_gemm_mx(&fc1, scale_rows, static_cast<int32_t>(call->activation), stream) != 0)
+  if (!want(UNISERVE_MOE_LAYER_GATHER)) {
+  } else if (by_expert != nullptr) {
+    gather_gemm_mx_by_expert(&fc1, *by_expert, static_cast<int32_t>(call->activation), stream);
+    if (int32_t status = launched(call, "gather_gemm_mx")) return status;
+  } else if (gather_gemm_mx(&fc1, scale_rows, static_cast<int32_t>(call->activation), stream) != 0) {
     return forward_error(call, "gather_gemm_mx", fc1);
+  }
 
   uniserve_quantize_mxfp8_call qg{};
   qg.input = at(v.gated);
   qg.out = at(v.gated_q);
   qg.scales = static_cast<uint8_t *>(at(v.gated_s));
-  qg.row_limit = static_cast<const int32_t *>(at(v.total_padded_tokens));
-  qg.rows = v.permuted_rows;
+  // (Without the sort: every route's row, at its expanded position.)
+  qg.row_limit = by_expert != nullptr ? nullptr : static_cast<const int32_t *>(at(v.total_padded_tokens));
+  qg.rows = by_expert != nullptr ? by_expert->routes : v.permuted_rows;
   qg.width = call->intermediate;
   qg.input_dtype = UNISERVE_DTYPE_BF16;
   if (!want(UNISERVE_MOE_LAYER_QUANTIZE_GATED)) {
@@ -204,8 +211,13 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   fc2.out_dtype = UNISERVE_DTYPE_BF16;
   fc2.multiprocessors = call->multiprocessors;
   fc2.weight_scale_layout = call->weight_scale_layout;
-  if (want(UNISERVE_MOE_LAYER_ROUTE) && route_gemm_mx(&fc2, scale_rows, stream) != 0)
+  if (!want(UNISERVE_MOE_LAYER_ROUTE)) {
+  } else if (by_expert != nullptr) {
+    route_gemm_mx_by_expert(&fc2, *by_expert, stream);
+    if (int32_t status = launched(call, "route_gemm_mx")) return status;
+  } else if (route_gemm_mx(&fc2, scale_rows, stream) != 0) {
     return forward_error(call, "route_gemm_mx", fc2);
+  }
   return 0;
 }
 
@@ -251,14 +263,14 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (call->tokens == 0) return 0;
     if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
     const int32_t activation = static_cast<int32_t>(call->activation);
-    // bf16 and e4m3 at decode sizes: no sort - the fused front end routes, and the products'
-    // workgroups each serve one local expert, finding its routes in `ids` (rows at expanded
-    // positions).
+    // Decode sizes: no sort - the fused front end routes, and the products' workgroups each serve
+    // one local expert, finding its routes in `ids` (rows at expanded positions).
     const int64_t routes = call->tokens * call->top;
     const bool front = front_fits(call->tokens, call->experts, call->hidden_size, call->top, local_experts);
-    const bool by_expert = front && !mx &&
+    const bool by_expert = front &&
                            expert_stream_fits(routes, local_experts, call->hidden_size, call->intermediate, true) &&
-                           expert_stream_fits(routes, local_experts, call->intermediate, call->hidden_size, false);
+                           expert_stream_fits(routes, local_experts, call->intermediate, call->hidden_size, false) &&
+                           (!mx || (call->hidden_size % 256 == 0 && call->intermediate % 256 == 0));
 
     char *ws = static_cast<char *>(workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
@@ -359,7 +371,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
 
     // 4-5. The two products.
     if (mx) {
-      if (int32_t status = run_mx_products(call, v, ws, want, stream)) return status;
+      const ExpertRouting routing{ids, call->live_tokens, routes, call->top, call->local_offset, local_experts};
+      if (int32_t status = run_mx_products(call, v, ws, want, stream, by_expert ? &routing : nullptr)) return status;
     } else if (by_expert && !fp8) {
       ExpertStream e{};
       e.ids = ids;
