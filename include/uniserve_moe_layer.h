@@ -58,11 +58,12 @@ UNISERVE_EXTERN_C int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t h
                                                        int64_t intermediate, int64_t weight_dtype);
 
 /// Offsets (bytes from `workspace`) of the intermediate tensors, for callers that read them:
-/// scores, ids, weights, the seven sort maps, gated rows, products. bf16 and e4m3 weights at
-/// decode sizes (the fused front end, at most 4096 routes, fewer than 24 per local expert) skip the
-/// sort: then expanded_to_permuted holds each route's own index (token * top + k) where the route
-/// is live and in the window and -1 elsewhere, the other six maps are not written, and gated rows
-/// and products (and e4m3's gated codes and scales) sit at those expanded positions.
+/// scores, ids, weights, the seven sort maps, gated rows, products. At decode sizes (the fused
+/// front end, at most 4096 routes, fewer than 24 per local expert) the layer skips the sort, for
+/// every weight type: then expanded_to_permuted holds each route's own index (token * top + k)
+/// where the route is live and in the window and -1 elsewhere, the other six maps are not
+/// written, and gated rows and products (and the quantised gated rows and their scales) sit at
+/// those expanded positions.
 struct uniserve_moe_layer_views {
   int64_t ticket;              ///< [256] u32 counters of the fused decode front end (offset 0)
   int64_t scores;              ///< [tokens, experts] bf16
