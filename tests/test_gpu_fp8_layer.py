@@ -300,6 +300,26 @@ def test_layer_is_deterministic(device):
     np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("tokens,hidden,intermediate", [(64, 2048, 768), (1, 4096, 1536), (20, 2048, 768)])
+def test_decode_front_quantises_like_the_quantiser(device, tokens, hidden, intermediate):
+    """At decode sizes the fused front end also quantises the hidden rows for e4m3 layers: its codes
+    and scales are the stand-alone quantiser's, bit for bit."""
+    announce("front quantisation", tokens, hidden)
+    experts, top = 128, 8
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 70 + tokens)
+    q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+    q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f8e4m3")
+    d = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    layer(x, router, d(q1), d(q2), up_gate_scales=d(s1), down_scales=d(s2))
+    want_q, want_s = ops.quantize_fp8(x)
+    torch.cuda.synchronize()
+    got_q = layer.view("hidden_q", torch.uint8, (tokens, hidden)).cpu().numpy()
+    got_s = layer.view("hidden_s", torch.float32, (tokens, hidden // 128)).cpu().numpy()
+    np.testing.assert_array_equal(got_q, want_q.cpu().numpy())
+    np.testing.assert_array_equal(got_s.view(np.uint32), want_s.cpu().numpy().view(np.uint32))
+
+
 def test_prefill_fc1_quantises_like_the_quantiser(device):
     """At prefill shapes the layer's FC1 writes the gated rows straight in FC2's e4m3 form; codes
     and scales of every live row equal the stand-alone FC1 (bf16 out) followed by quantize_fp8."""

@@ -101,6 +101,28 @@ __device__ __forceinline__ uint2 e4m3_eight_of_bf16(const float (&v)[8], float s
   return e4m3_eight(v, scale);
 }
 
+/// One 128-channel group of a bf16 row as e4m3 codes and its FP32 scale (amax / 448, 1 for an
+/// all-zero group), 16 lanes per group (lane `sub` holds channels 8 sub .. 8 sub + 7): the
+/// activation quantiser's arithmetic, shared by every kernel that quantises hidden rows. Returns
+/// the scale (every lane of the group holds it).
+__device__ __forceinline__ float quantize_bf16_group(const uint16_t *group, uint8_t *codes, float *scale_out, int sub) {
+  const u32x4 packed = *reinterpret_cast<const u32x4 *>(group + sub * 8);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(packed[j] << 16);
+    v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+  amax = row16_max(amax);
+  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+  *reinterpret_cast<uint2 *>(codes + sub * 8) = e4m3_eight_of_bf16(v, scale);
+  if (sub == 0) *scale_out = scale;
+  return scale;
+}
+
 struct GroupedFp8Params {
   const uint8_t *act;           ///< FC1: hidden [tokens, K]; FC2: rows [permuted_rows, K], e4m3
   const float *act_scales;      ///< [rows of act, K / 128]

@@ -56,29 +56,24 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
        group += stride) {
     const int64_t row = group / groups_per_row;
     const int64_t column = (group % groups_per_row) * 128 + sub * 8;
-    float v[8];
+    float scale;
     if (p.input_f32) {
       const float *src = static_cast<const float *>(p.input) + row * p.width + column;
       const float4 lo = *reinterpret_cast<const float4 *>(src);
       const float4 hi = *reinterpret_cast<const float4 *>(src + 4);
-      v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-      v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+      float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      float amax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+      amax = row16_max(amax);
+      scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+      *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, scale);
+      if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
     } else {
-      const u32x4 packed = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p.input) + row * p.width + column);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[2 * j] = __uint_as_float(packed[j] << 16);
-        v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
-      }
+      const int64_t group_first = row * p.width + column - sub * 8;
+      scale = quantize_bf16_group(static_cast<const uint16_t *>(p.input) + group_first, p.out + group_first,
+                                  p.scales + row * groups_per_row + column / 128, sub);
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
-    amax = row16_max(amax);
-    const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-    *reinterpret_cast<uint2 *>(p.out + row * p.width + column) =
-        p.input_f32 ? e4m3_eight(v, scale) : e4m3_eight_of_bf16(v, scale);
-    if (sub == 0) p.scales[row * groups_per_row + column / 128] = scale;
     if (p.route_scales != nullptr) {
       for (int64_t k = sub; k < p.top; k += 16) {
         const int32_t at = p.expanded_to_permuted[row * p.top + k];

@@ -31,6 +31,7 @@ extern "C" int uniserve_front_trace_read(unsigned long long *out) {
 }
 #endif
 #include "common.hpp"
+#include "grouped_fp8.hpp"
 #include "moe_front.hpp"
 #include "sort_small.hpp"
 #include "topk_route.hpp"
@@ -123,8 +124,28 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   }
   __syncthreads();
 
+  // e4m3 layers: the hidden rows' quantisation, off the routing's path - each workgroup's share of
+  // its token block's 128-channel groups (group g to expert block g % expert blocks), done once the
+  // workgroup has nothing else to do (the quantiser's arithmetic: codes bit for bit its own).
+  auto quantize_share = [&]() {
+    if (p.hidden_codes == nullptr) return;
+    const int64_t groups_per_row = p.hidden / 128;
+    const int64_t block_groups = kTile * groups_per_row;
+    const int64_t step = static_cast<int64_t>(kThreads / 16) * gridDim.y;
+    for (int64_t g = blockIdx.y + static_cast<int64_t>(threadIdx.x / 16) * gridDim.y; g < block_groups; g += step) {
+      const int64_t row = static_cast<int64_t>(blockIdx.x) * kTile + g / groups_per_row;
+      if (row >= p.tokens) continue;
+      const int64_t column = (g % groups_per_row) * 128;
+      quantize_bf16_group(p.x + row * p.hidden + column, p.hidden_codes + row * p.hidden + column,
+                          p.hidden_scales + row * groups_per_row + g % groups_per_row, static_cast<int>(threadIdx.x & 15));
+    }
+  };
+
   // 2. The last of the token block's tiles routes its tokens, one per 32-lane half.
-  if (!last_ticket(p.ticket + 1 + blockIdx.x, gridDim.y, &flag)) return;
+  if (!last_ticket(p.ticket + 1 + blockIdx.x, gridDim.y, &flag)) {
+    quantize_share();
+    return;
+  }
   UNISERVE_TRACE(1);
   const int half = static_cast<int>(threadIdx.x) / topk::kHalf;
   if (half < kTile) {
@@ -146,14 +167,19 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
       const bool visible = route < live && local >= 0 && local < p.sort.local_experts;
       p.sort.expanded_to_permuted[route] = visible ? static_cast<int32_t>(route) : -1;
     }
+    quantize_share();
     return;
   }
 
   // 3. The last of the token blocks sorts every route.
-  if (!last_ticket(p.ticket, gridDim.x, &flag)) return;
+  if (!last_ticket(p.ticket, gridDim.x, &flag)) {
+    quantize_share();
+    return;
+  }
   UNISERVE_TRACE(4);
   sort::small_sort<false, true>(p.sort, front_lds);
   UNISERVE_TRACE(3);
+  quantize_share();
 }
 
 }  // namespace

@@ -35,6 +35,10 @@ struct FrontParams {
   /// expanded index where it is live and in the window, -1 elsewhere (for products that find their
   /// routes themselves and keep rows at expanded positions), and nothing else of the sort's.
   int32_t sort_routes;
+  /// Or null: the hidden rows as e4m3 codes [tokens, hidden] with a scale per 128 channels
+  /// [tokens, hidden / 128] - the activation quantiser's output, made by this launch.
+  uint8_t *hidden_codes;
+  float *hidden_scales;
 };
 
 /// Whether one launch serves these extents: the router's split-contraction tiles, a router of at

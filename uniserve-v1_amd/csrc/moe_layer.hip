@@ -272,6 +272,10 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
                            expert_stream_fits(routes, local_experts, call->intermediate, call->hidden_size, false) &&
                            (!mx || (call->hidden_size % 256 == 0 && call->intermediate % 256 == 0));
 
+    // e4m3 at those sizes: the front end also quantises the hidden rows (QUANTIZE_HIDDEN then
+    // launches nothing).
+    const bool front_quantizes = front && fp8 && !v.route_scales && call->hidden_size % 128 == 0;
+
     char *ws = static_cast<char *>(workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -324,6 +328,10 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         while ((1ll << bits) <= local_experts) ++bits;
         sp.key_bits = bits;
         fp.sort_routes = by_expert ? 0 : 1;
+        if (front_quantizes) {
+          fp.hidden_codes = static_cast<uint8_t *>(at(v.hidden_q));
+          fp.hidden_scales = static_cast<float *>(at(v.hidden_s));
+        }
         launch_front(fp, s);
         if (int32_t status = launched(call, "router, topk and sort")) return status;
       }
@@ -450,7 +458,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       qx.width = call->hidden_size;
       qx.input_dtype = UNISERVE_DTYPE_BF16;
       qx.group = 128;
-      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN)) {
+      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || front_quantizes) {
       } else if (scale_rows != 0) {
         launch_quantize_fp8_routes(static_cast<const uint16_t *>(call->hidden), static_cast<uint8_t *>(at(v.hidden_q)),
                                    static_cast<float *>(at(v.hidden_s)), static_cast<float *>(at(v.hidden_route_s)), e2p,
