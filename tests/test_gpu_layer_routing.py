@@ -45,6 +45,10 @@ ROUTED = {
     "bf16 decode, every expert, map + load only": (64, 2048, 128, 8, 768, "bf16", None, None),
     "bf16 decode, map + load + window + live": (64, 2048, 128, 8, 768, "bf16", (40, 64), 50),
     "bf16 one token, map + load + window": (1, 2048, 128, 8, 768, "bf16", (32, 64), None),
+    # fewer routes than local experts, some experts named twice: the compact expert-major grid
+    "bf16 8 tokens, map + load + window + live": (8, 2048, 128, 8, 768, "bf16", (16, 96), 6),
+    "fp8 8 tokens, map + load + window": (8, 2048, 128, 8, 768, "f8e4m3", (16, 96), None),
+    "mx 8 tokens, map + load + window": (8, 2048, 128, 8, 768, "f4e2m1", (16, 96), None),
 }
 
 
