@@ -59,8 +59,8 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) sum[j] = 0.0f;
   // Routes in batches of kBatch: the batch's map entries and weights, then its route rows, are
-  // loaded before any is used (two round trips per batch, not two per route); the sum still
-  // takes the routes in order.
+  // loaded before any is used (two round trips per batch, not two per route; one in the expanded
+  // layout); the sum still takes the routes in order.
   constexpr int kBatch = 8;
   for (int64_t k0 = 0; k0 < p.top; k0 += kBatch) {
     int32_t entry[kBatch];
@@ -75,7 +75,9 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
     uint4 packed[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const bool visible = entry[u] >= 0 && entry[u] < p.routes_rows;
+      // Expanded rows sit at known places: loaded beside their map entries (one round trip), an
+      // invisible route's row read and then ignored.
+      const bool visible = p.expanded ? k0 + u < p.top : entry[u] >= 0 && entry[u] < p.routes_rows;
       const int64_t row = p.expanded ? token * p.top + k0 + u : entry[u];
       if (visible) {
         const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(routes + row * p.hidden + column));
