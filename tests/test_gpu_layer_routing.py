@@ -75,6 +75,8 @@ def test_layer_routing_options_against_the_oracle(device, case):
     got = bf16_values(out)
     ids = layer.view("ids", torch.int32, (tokens, top)).cpu().numpy()
     scores = bf16_bits(layer.view("scores", torch.bfloat16, (tokens, experts)))
+    # Every counter the call's launches meet through (the ticket view) is left zero.
+    assert int(layer.workspace[: layer.views.scores].count_nonzero()) == 0
 
     host_load = np.full(experts, 5, np.int64)
     want_bits, want_ids, _, _, want_scores = O.moe_layer(
