@@ -125,10 +125,10 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_
 
 /// The layer's launches in order; the quantiser steps launch nothing for bf16 weights,
 /// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised, and
-/// QUANTIZE_HIDDEN nothing for e4m3 at decode sizes (the ROUTER launch quantises). At decode
-/// sizes (at most 4096 routes over at most 512 local experts, a router of at most 1024 experts)
-/// ROUTER launches the router, topk and sort as one kernel (no sort where the layer skips it),
-/// and TOPK and SORT launch nothing.
+/// QUANTIZE_HIDDEN nothing for e4m3 and MXFP4 at decode sizes (the ROUTER launch quantises). At
+/// decode sizes (at most 4096 routes over at most 512 local experts, a router of at most 1024
+/// experts) ROUTER launches the router, topk and sort as one kernel (no sort where the layer
+/// skips it), and TOPK and SORT launch nothing.
 enum uniserve_moe_layer_step {
   UNISERVE_MOE_LAYER_ROUTER = 0,
   UNISERVE_MOE_LAYER_TOPK = 1,

@@ -29,6 +29,10 @@ def test_mxfp8_quantiser_is_bit_exact(device):
     x[3, :64] = 0.0
     x[7, 5] = 3.0e38
     x[9, 32:64] = 1.0e-39                                 # subnormal block: exponent clamps at -127
+    # Blocks whose amax sits on either side of 448 * 2^e (bf16 neighbours of 448, 3.5 and 7 / 2^100).
+    x[11, 0:32], x[11, 32], x[11, 64] = 0.25, 448.0, 450.0
+    x[11, 96], x[11, 128] = 3.5, 3.515625
+    x[12, 0], x[12, 32] = 7.0 * 2.0**-100, 7.25 * 2.0**-100
     bits = O.bf16_encode(x)
     t = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(device)
     q, s = ops.quantize_mxfp8(t)
@@ -164,6 +168,27 @@ def test_mx_layer_against_the_oracle(device, case):
         np.testing.assert_array_equal(ids[rows], want_ids)
         want = O.bf16_decode(want_bits).astype(np.float64)
     assert_bf16_bar(got[rows], want, case, max_rel=4e-2)
+
+
+@pytest.mark.parametrize("tokens,hidden,intermediate", [(64, 2048, 768), (1, 4096, 1536), (20, 2048, 768)])
+def test_decode_front_quantises_like_the_mxfp8_quantiser(device, tokens, hidden, intermediate):
+    """At decode sizes the fused front end also quantises the hidden rows for MXFP4 layers: its
+    codes and E8M0 bytes are the stand-alone MXFP8 quantiser's, bit for bit (a few rows scaled up
+    and down by powers of two so that blocks span many exponents)."""
+    announce("front mx quantisation", tokens, hidden)
+    experts, top = 128, 8
+    x, router, host_w = mx_layer_inputs(device, tokens, hidden, experts, intermediate, 90 + tokens)
+    x[::3] *= 2.0**40
+    x[1::5] *= 2.0**-60
+    w1, s1, w2, s2 = on(device, host_w)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f4e2m1")
+    layer(x, router, w1, w2, up_gate_scales=s1, down_scales=s2)
+    want_q, want_s = ops.quantize_mxfp8(x)
+    torch.cuda.synchronize()
+    got_q = layer.view("hidden_q", torch.uint8, (tokens, hidden)).cpu().numpy()
+    got_s = layer.view("hidden_s", torch.uint8, (tokens, hidden // 32)).cpu().numpy()
+    np.testing.assert_array_equal(got_q, want_q.cpu().numpy())
+    np.testing.assert_array_equal(got_s, want_s.cpu().numpy())
 
 
 def sampled_mx_layer(x_bits, ids, weights, host_w, experts, top):

@@ -51,20 +51,6 @@ struct MxQuantParams {
   int64_t stage_rows;
 };
 
-/// The E8M0 byte of a block: the smallest power of two 2^e with amax <= limit * 2^e, e in
-/// [-127, 127]; an all-zero or infinite block takes 2^0. The division is IEEE (the library is
-/// built with correctly rounded division) and the comparisons are exact, so the host rule holds
-/// bit for bit.
-__device__ __forceinline__ uint32_t mx_scale(float amax, float limit) {
-  if (!(amax > 0.0f) || __builtin_isinf(amax)) return 127u;
-  int e;
-  frexpf(amax / limit, &e);
-  while (e > -127 && amax <= ldexpf(limit, e - 1)) --e;
-  while (e < 127 && amax > ldexpf(limit, e)) ++e;
-  if (e < -127) e = -127;  // a subnormal block: 2^-127 already holds it
-  return static_cast<uint32_t>(e + 127);
-}
-
 /// Four lanes per 32-channel block, eight channels each; a grid-stride loop that stops at the
 /// device-side row limit.
 __global__ void __launch_bounds__(kQuantThreads) quantize_mxfp8_kernel(MxQuantParams p) {
@@ -92,14 +78,7 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_mxfp8_kernel(MxQuantPa
         v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
       }
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 1, 4));
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 2, 4));
-    const uint32_t scale = mx_scale(amax, 448.0f);
-    // A power of two: the division is exact and no quotient exceeds 448.
-    *reinterpret_cast<uint2 *>(p.out + row * p.width + column) = e4m3_eight(v, ldexpf(1.0f, static_cast<int>(scale) - 127));
+    const uint32_t scale = mxfp8_eight(v, p.out + row * p.width + column);
     if (sub == 0 && p.scales != nullptr) p.scales[block] = static_cast<uint8_t>(scale);
     if (p.stage_scales != nullptr) {
       const int64_t b = block % blocks_per_row;

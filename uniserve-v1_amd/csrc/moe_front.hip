@@ -32,6 +32,7 @@ extern "C" int uniserve_front_trace_read(unsigned long long *out) {
 #endif
 #include "common.hpp"
 #include "grouped_fp8.hpp"
+#include "grouped_mx.hpp"
 #include "moe_front.hpp"
 #include "sort_small.hpp"
 #include "topk_route.hpp"
@@ -124,11 +125,34 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   }
   __syncthreads();
 
-  // e4m3 layers: the hidden rows' quantisation, off the routing's path - each workgroup's share of
-  // its token block's 128-channel groups (group g to expert block g % expert blocks), done once the
-  // workgroup has nothing else to do (the quantiser's arithmetic: codes bit for bit its own).
-  auto quantize_share = [&]() {
+  // e4m3 and MXFP4 layers: the hidden rows' quantisation, off the routing's path - each workgroup's
+  // share of its token block's 128-channel groups (group g to expert block g % expert blocks), or
+  // 32-channel MXFP8 blocks, done once the workgroup has nothing else to do (the quantisers'
+  // arithmetic: codes bit for bit their own).
+  auto quantize_share = [&]() __attribute__((always_inline)) {
     if (p.hidden_codes == nullptr) return;
+    if (p.hidden_mx_scales != nullptr) {
+      // MXFP8: blocks of 32 channels, four lanes each (block b to expert block b % expert blocks).
+      const int64_t blocks_per_row = p.hidden / 32;
+      const int64_t block_blocks = kTile * blocks_per_row;
+      const int64_t step = static_cast<int64_t>(kThreads / 4) * gridDim.y;
+      const int sub = static_cast<int>(threadIdx.x & 3);
+      for (int64_t b = blockIdx.y + static_cast<int64_t>(threadIdx.x / 4) * gridDim.y; b < block_blocks; b += step) {
+        const int64_t row = static_cast<int64_t>(blockIdx.x) * kTile + b / blocks_per_row;
+        if (row >= p.tokens) continue;
+        const int64_t column = (b % blocks_per_row) * 32 + sub * 8;
+        const u32x4 packed = *reinterpret_cast<const u32x4 *>(p.x + row * p.hidden + column);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[2 * j] = __uint_as_float(packed[j] << 16);
+          v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
+        }
+        const uint32_t scale = mxfp8_eight(v, p.hidden_codes + row * p.hidden + column);
+        if (sub == 0) p.hidden_mx_scales[row * blocks_per_row + b % blocks_per_row] = static_cast<uint8_t>(scale);
+      }
+      return;
+    }
     const int64_t groups_per_row = p.hidden / 128;
     const int64_t block_groups = kTile * groups_per_row;
     const int64_t step = static_cast<int64_t>(kThreads / 16) * gridDim.y;

@@ -39,6 +39,9 @@ struct FrontParams {
   /// [tokens, hidden / 128] - the activation quantiser's output, made by this launch.
   uint8_t *hidden_codes;
   float *hidden_scales;
+  /// With hidden_codes and instead of hidden_scales: MXFP8 blocks of 32 channels, their E8M0
+  /// bytes [tokens, hidden / 32] - the MXFP8 quantiser's output.
+  uint8_t *hidden_mx_scales;
 };
 
 /// Whether one launch serves these extents: the router's split-contraction tiles, a router of at

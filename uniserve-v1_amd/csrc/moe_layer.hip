@@ -119,7 +119,8 @@ namespace {
 /// `by_expert` set: the decode products without a sort (rows at expanded positions).
 template <class Want>
 int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_layer_views &v, char *ws,
-                        const Want &want, void *stream, const uniserve::ExpertRouting *by_expert) {
+                        const Want &want, void *stream, const uniserve::ExpertRouting *by_expert,
+                        bool hidden_quantised) {
   using namespace uniserve;
   auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
   const auto *t2e = static_cast<const int32_t *>(at(v.tile_to_expert));
@@ -136,7 +137,7 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   qx.rows = call->tokens;
   qx.width = call->hidden_size;
   qx.input_dtype = UNISERVE_DTYPE_BF16;
-  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN)) {
+  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || hidden_quantised) {
   } else if (scale_rows != 0) {
     // Each token's scale words go to its routes' permuted rows.
     launch_quantize_mxfp8(call->hidden, false, static_cast<uint8_t *>(at(v.hidden_q)), nullptr, nullptr, call->tokens,
@@ -272,9 +273,9 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
                            expert_stream_fits(routes, local_experts, call->intermediate, call->hidden_size, false) &&
                            (!mx || (call->hidden_size % 256 == 0 && call->intermediate % 256 == 0));
 
-    // e4m3 at those sizes: the front end also quantises the hidden rows (QUANTIZE_HIDDEN then
-    // launches nothing).
-    const bool front_quantizes = front && fp8 && !v.route_scales && call->hidden_size % 128 == 0;
+    // e4m3 and MXFP4 at those sizes: the front end also quantises the hidden rows (QUANTIZE_HIDDEN
+    // then launches nothing).
+    const bool front_quantizes = front && (fp8 || mx) && !v.route_scales && call->hidden_size % 128 == 0;
 
     char *ws = static_cast<char *>(workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
@@ -330,7 +331,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         fp.sort_routes = by_expert ? 0 : 1;
         if (front_quantizes) {
           fp.hidden_codes = static_cast<uint8_t *>(at(v.hidden_q));
-          fp.hidden_scales = static_cast<float *>(at(v.hidden_s));
+          if (mx) fp.hidden_mx_scales = static_cast<uint8_t *>(at(v.hidden_s));
+          else fp.hidden_scales = static_cast<float *>(at(v.hidden_s));
         }
         launch_front(fp, s);
         if (int32_t status = launched(call, "router, topk and sort")) return status;
@@ -380,7 +382,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     // 4-5. The two products.
     if (mx) {
       const ExpertRouting routing{ids, call->live_tokens, routes, call->top, call->local_offset, local_experts};
-      if (int32_t status = run_mx_products(call, v, ws, want, stream, by_expert ? &routing : nullptr)) return status;
+      if (int32_t status = run_mx_products(call, v, ws, want, stream, by_expert ? &routing : nullptr, front_quantizes))
+        return status;
     } else if (by_expert && !fp8) {
       ExpertStream e{};
       e.ids = ids;
