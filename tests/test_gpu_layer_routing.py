@@ -49,6 +49,11 @@ ROUTED = {
     "bf16 8 tokens, map + load + window + live": (8, 2048, 128, 8, 768, "bf16", (16, 96), 6),
     "fp8 8 tokens, map + load + window": (8, 2048, 128, 8, 768, "f8e4m3", (16, 96), None),
     "mx 8 tokens, map + load + window": (8, 2048, 128, 8, 768, "f4e2m1", (16, 96), None),
+    # a window of 16 experts: 24 or more routes per local expert, so the decode front end (which
+    # still quantises the hidden rows) hands over to the sort and the tiled products
+    "fp8 decode, narrow window": (64, 2048, 128, 8, 768, "f8e4m3", (8, 16), None),
+    "mx decode, narrow window": (64, 2048, 128, 8, 768, "f4e2m1", (8, 16), None),
+    "bf16 decode, narrow window + live": (64, 2048, 128, 8, 768, "bf16", (8, 16), 40),
 }
 
 
