@@ -49,9 +49,9 @@ def parse():
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--config", default="30b-decode-bf16", choices=sorted(CONFIGS))
     parser.add_argument("--extra", action="store_true", help="also measure every other BASELINE config")
-    parser.add_argument("--also", default="30b-prefill-fp8",
+    parser.add_argument("--also", default="30b-prefill-fp8,30b-prefill-bf16",
                         help="comma-separated configs measured briefly beside the main one (default: the fp8 "
-                             "prefill target's config); '' for none")
+                             "and bf16 prefill targets' config); '' for none")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     parser.add_argument("--cpu-runs", type=int, default=3)
     parser.add_argument("--traffic-summary", metavar="DIR",
