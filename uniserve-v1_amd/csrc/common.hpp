@@ -14,14 +14,6 @@
 
 #include "uniserve_abi.h"
 
-// Probe points of latency-bound routines (a build with UNISERVE_FRONT_TRACE records timestamps at
-// them; the product build compiles them to nothing).
-#ifndef UNISERVE_TRACE
-#define UNISERVE_TRACE(slot) \
-  do {                       \
-  } while (0)
-#endif
-
 namespace uniserve {
 
 constexpr int kWave = 64;
@@ -63,6 +55,15 @@ int32_t launched(const Call *call, const char *what) {
   const hipError_t status = hipGetLastError();
   if (status == hipSuccess) return 0;
   return UNISERVE_REFUSE(call, "%s could not start: %s", what, hipGetErrorString(status));
+}
+
+/// The prefill kernels address gathered activation rows (FC1's token rows) as 32-bit byte offsets
+/// from the array's base (the scalar-base form of global_load_lds): an array of `rows` rows of
+/// `row_bytes` bytes is served when it lies below 4 GiB. (FC2's rows are addressed from their
+/// tile's first row and have no such limit.)
+constexpr int64_t kDmaArrayBytes = int64_t{1} << 32;
+inline bool dma_rows_fit(int64_t rows, int64_t row_bytes) {
+  return rows >= 0 && row_bytes >= 0 && (row_bytes == 0 || rows <= kDmaArrayBytes / row_bytes);
 }
 
 // ---- element conversions ---------------------------------------------------------------------------

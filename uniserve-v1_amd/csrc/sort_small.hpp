@@ -92,7 +92,6 @@ __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
   for (int u = 0; u < kSmallGroups; ++u) peers[u] = match_any(static_cast<uint32_t>(e[u] + 1), p.key_bits);
   for (int i = threadIdx.x; i < kSortWaves * E; i += kSortThreads) rows[i] = 0;
   __syncthreads();
-  UNISERVE_TRACE(10);
 
   // 1. This wavefront's counts.
   int32_t *mine = rows + wave * E;
@@ -102,7 +101,6 @@ __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
     __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
-  UNISERVE_TRACE(11);
 
   // 2. Totals, the scan of the tile counts, the start rows.
   const int ex = static_cast<int>(threadIdx.x);
@@ -118,7 +116,6 @@ __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
   }
   if (lane == kWave - 1) wave_tiles[wave] = inclusive;
   __syncthreads();
-  UNISERVE_TRACE(12);
   int32_t carried = 0;
   for (int w = 0; w < wave; ++w) carried += wave_tiles[w];
   if (ex < E) {
@@ -137,7 +134,6 @@ __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
     p.num_non_exiting_tiles[0] = carried + inclusive;
   }
   __syncthreads();
-  UNISERVE_TRACE(13);
 
   // 3. Tile tables (thread e for expert e) and padding rows (one wavefront per expert); then the
   // placement.

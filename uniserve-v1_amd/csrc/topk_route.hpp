@@ -134,7 +134,6 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
                                   : -__builtin_inff();
   }
 
-  UNISERVE_TRACE(20);
   float maximum = values[0];
 #pragma unroll
   for (int it = 0; it < kIter; ++it) maximum = maximum > values[it] ? maximum : values[it];
@@ -158,7 +157,6 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
 #pragma unroll
   for (int it = 0; it < kIter; ++it) values[it] = values[it] / sum;
 
-  UNISERVE_TRACE(21);
   // `top` rounds of a (value, lower id) arg-max; lane j keeps round j's pick. A round's pick is
   // the largest probability among the experts not yet taken, the lowest id among equal ones (the
   // reference's (value, lower id) butterfly, topk_softmax.cu:152-182): the maximum value by a
@@ -199,7 +197,6 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
     if (best_expert != INT_MAX && (best_expert & (kHalf - 1)) == lane) taken |= 1u << (best_expert / kHalf);
   }
 
-  UNISERVE_TRACE(22);
   float weight = picked;
   if (renormalize) {
     // The butterfly over the next power of two of `top` lanes, lanes past `top` holding zero.
