@@ -52,7 +52,8 @@ struct uniserve_moe_layer_call {
 
 /// Workspace bytes the call needs for these extents, or -1 for extents it does not serve. The
 /// workspace's first 1024 bytes (the `ticket` view) must be zero before the first call that uses
-/// it; every call leaves them zero (the rest needs no initialisation).
+/// it; every call leaves them zero (the rest needs no initialisation). A call at decode sizes that
+/// finds them not zero fails loudly: its output is NaN, and the words are cleared for the next call.
 UNISERVE_EXTERN_C int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_size,
                                                        int64_t experts, int64_t top,
                                                        int64_t intermediate, int64_t weight_dtype);
@@ -116,9 +117,10 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_cal
 /// `workspace` and `workspace_bytes` are ignored, everything else is read as uniserve_moe_layer
 /// reads it. Extents whose intermediates (uniserve_moe_layer_workspace) exceed the scratch are
 /// refused with a message. Nothing is allocated. The first call on each GPU looks the array's
-/// address up (hipGetSymbolAddress) and clears its counter word on the call's stream: make it
-/// outside stream capture. Every later call finds the counter zero (each call leaves it so) and
-/// needs nothing else cleared: every other intermediate is written before it is read. All calls on
+/// address up (hipGetSymbolAddress, a host-side query) and issues nothing else: the array is
+/// zero-initialised storage, so its counter words start at zero, and every call leaves them zero;
+/// every other intermediate is written before it is read. Any call, the first included, may be
+/// made under stream capture (no memset is ever issued). All calls on
 /// one GPU share its array, so calls that overlap on one GPU (concurrent streams or threads) race;
 /// serialise them.
 UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_layer_call *call, void *stream);

@@ -139,6 +139,27 @@ def test_product_refusals():
     g.permuted_rows = 4
     assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "cannot hold" in message(g)
 
+    # The prefill kernels address gathered hidden rows with 32-bit offsets: a hidden array of
+    # exactly 4 GiB passes that check (and meets the next refusal), one row more is refused.
+    g.hidden_size, g.permuted_rows = 4096, 4
+    g.tokens = (1 << 32) // (4096 * 2)
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "cannot hold" in message(g)
+    g.tokens += 1
+    assert lib.uniserve_gather_gemm(ctypes.byref(g), None) != 0 and "below 4 GiB" in message(g)
+    for call_type, entry, hidden in ((abi.GatherFp8Call, lib.uniserve_gather_gemm_fp8, 4096),
+                                     (abi.GatherMxCall, lib.uniserve_gather_gemm_mx, 4096)):
+        c = call_type()
+        for name in ("hidden", "hidden_scales", "weights", "weight_scales", "out", "tile_to_expert",
+                     "tile_to_limit", "permuted_to_expanded", "num_non_exiting_tiles"):
+            setattr(c, name, ctypes.addressof(buf))
+        c.out_dtype, c.multiprocessors, c.hidden_size, c.width, c.top, c.experts = abi.DTYPE["bf16"], 256, hidden, 1536, 8, 128
+        if hasattr(c, "block_n"):
+            c.block_n = c.block_k = 128
+        c.permuted_rows, c.tokens = 128, (1 << 32) // hidden
+        assert entry(ctypes.byref(c), None) != 0 and "whole 128-row tiles" in message(c)
+        c.tokens += 1
+        assert entry(ctypes.byref(c), None) != 0 and "below 4 GiB" in message(c)
+
     r = abi.RouteCall()
     r.dtype = abi.DTYPE["f32"]
     assert lib.uniserve_route_gemm(ctypes.byref(r), None) != 0 and "bf16 only" in message(r)

@@ -114,8 +114,13 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
       return r < rows ? first + r : first;
     }
   };
+  // The activation DMA's base: FC2's rows are the tile's own, addressed from the tile's first row,
+  // so their 32-bit lane offsets stay under 128 rows whatever the array's size; FC1's gathered
+  // token rows are addressed from the array, which the hosts hold below 4 GiB (dma_rows_fit).
+  const uint8_t *act_tile = p.act + (kGated ? 0 : first * p.K);
+  auto act_row = [&](int r) -> int64_t { return kGated ? source_row(r) : source_row(r) - first; };
 
-  // ---- DMA sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
+  // ---- DMA sources (32-bit lane offsets from wave-uniform bases) ----
   // Wave w's instruction i fills rows 32 w + 8 i + l / 8 of both the activation and the weight
   // stage, lane l bringing logical chunk (l % 8) ^ key(row) into physical chunk l % 8; its scale
   // instruction brings the scales of tile rows 32 w + l % 32 (lanes 32.. repeat them into the
@@ -131,7 +136,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 32 * wave + 8 * i + lane / 8;
-    a_off[i] = static_cast<uint32_t>(source_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
+    a_off[i] = static_cast<uint32_t>(act_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
     w_first[i] = static_cast<uint32_t>(weight_row(32 * wave + 8 * i));
   }
   // key(32 w + 8 i + l / 8) = (l / 16) % 4 + 4 (i % 2): one lane offset per instruction parity.
@@ -171,7 +176,7 @@ __global__ void __launch_bounds__(kThreads, 2) e4m3_kernel(PrefillParams p) {
     const uint32_t weight_lds = lds_address(st.weights + wave * 4 * kWave);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+      dma16(act_tile + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       dma16(sweep_weights + static_cast<int64_t>(w_first[i]) * p.K + static_cast<int64_t>(k) * 128, w_lane[i & 1],

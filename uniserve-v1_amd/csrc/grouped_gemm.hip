@@ -114,19 +114,6 @@ __device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
 }
 
 /// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
-// Development timing of each workgroup (s_memrealtime at its start, after its first stage and at
-// its end), in builds made with UNISERVE_PAIR_TRACE only.
-#ifdef UNISERVE_PAIR_TRACE
-#define STREAM_MARK(slot)                                                                                  \
-  do {                                                                                                     \
-    const unsigned lin = blockIdx.x + blockIdx.y * gridDim.x;                                              \
-    if (threadIdx.x == 0 && lin < 16384) pair_trace[lin][slot] = __builtin_amdgcn_s_memrealtime();         \
-  } while (0)
-#else
-#define STREAM_MARK(slot) \
-  do {                    \
-  } while (0)
-#endif
 /// kByExpert: workgroup x serves local expert x (grid: local experts x slices) and finds its rows
 /// itself - the routes whose id is the expert's, in route order, live ones only (each wavefront
 /// ballots a quarter of the routes into a list in LDS) - while its first weight stage is in
@@ -158,7 +145,6 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
     first = static_cast<int64_t>(tile) * kTileRows;
     rows = p.tile_to_limit[tile] - static_cast<int>(first);
   }
-  STREAM_MARK(0);
 
   int64_t n0, n1;
   if constexpr (kGated) {
@@ -263,7 +249,6 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
     for (int k = 0; k < stages; k += 2) {
       if (k + 1 < stages) load(odd, k + 1);
       compute(even);
-      if (k == 0) STREAM_MARK(1);
       if (k + 2 < stages) load(even, k + 2);
       if (k + 1 < stages) compute(odd);
     }
@@ -284,7 +269,6 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
       }
     }
   }
-  STREAM_MARK(3);
 }
 
 // ---- tiled kernel -----------------------------------------------------------------------------------------
@@ -498,6 +482,9 @@ int32_t gather_gemm_bf16(const uniserve_gather_call *call, int32_t activation, v
       return UNISERVE_REFUSE(call, "gather_gemm needs an intermediate width of whole 64-column blocks");
     if (call->tokens < 0 || call->top <= 0 || call->experts <= 0)
       return UNISERVE_REFUSE(call, "gather_gemm needs non-negative tokens and positive top and experts");
+    if (!dma_rows_fit(call->tokens, call->hidden_size * 2))
+      return UNISERVE_REFUSE(call, "gather_gemm serves hidden rows below 4 GiB (%lld tokens of %lld bytes)",
+                             static_cast<long long>(call->tokens), static_cast<long long>(call->hidden_size * 2));
     if (call->permuted_rows < call->tokens * call->top)
       return UNISERVE_REFUSE(call, "%lld permuted rows cannot hold %lld routes",
                              static_cast<long long>(call->permuted_rows),
@@ -528,15 +515,6 @@ int32_t gather_gemm_bf16(const uniserve_gather_call *call, int32_t activation, v
     return launched(call, "gather_gemm");
   });
 }
-
-#ifdef UNISERVE_PAIR_TRACE
-extern "C" int uniserve_pair_trace_read_bf16(unsigned long long *out, int clear) {
-  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(pair_trace), sizeof(pair_trace)) != hipSuccess) return 1;
-  static unsigned long long zeros[16384][8];
-  if (clear && hipMemcpyToSymbol(HIP_SYMBOL(pair_trace), zeros, sizeof(zeros)) != hipSuccess) return 1;
-  return 0;
-}
-#endif
 
 }  // namespace uniserve
 

@@ -88,7 +88,6 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_kernel(QuantParams p) 
 constexpr int kTileRows = 128;
 constexpr int kThreads = 256;
 
-
 __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
   uint2 packed;
   packed.x = pack_bf16x2(v[0], v[1]);
@@ -699,6 +698,9 @@ int32_t gather_gemm_fp8(const uniserve_gather_fp8_call *call, uint8_t *codes, fl
       return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs an intermediate width of whole 128-row blocks");
     if (call->tokens < 0 || call->top <= 0 || call->experts <= 0)
       return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs non-negative tokens and positive top and experts");
+    if (!dma_rows_fit(call->tokens, call->hidden_size))
+      return UNISERVE_REFUSE(call, "gather_gemm_fp8 serves hidden rows below 4 GiB (%lld tokens of %lld bytes)",
+                             static_cast<long long>(call->tokens), static_cast<long long>(call->hidden_size));
     if (call->permuted_rows < call->tokens * call->top || call->permuted_rows % kTileRows != 0)
       return UNISERVE_REFUSE(call, "gather_gemm_fp8 needs whole 128-row tiles that hold every route");
     const int64_t max_tiles = call->permuted_rows / kTileRows;
@@ -799,14 +801,5 @@ int32_t route_gemm_fp8(const uniserve_route_fp8_call *call, int64_t scale_rows, 
     return launched(call, "route_gemm_fp8");
   });
 }
-
-#ifdef UNISERVE_PAIR_TRACE
-extern "C" int uniserve_pair_trace_read_fp8(unsigned long long *out, int clear) {
-  if (hipMemcpyFromSymbol(out, HIP_SYMBOL(pair_trace), sizeof(pair_trace)) != hipSuccess) return 1;
-  static unsigned long long zeros[16384][8];
-  if (clear && hipMemcpyToSymbol(HIP_SYMBOL(pair_trace), zeros, sizeof(zeros)) != hipSuccess) return 1;
-  return 0;
-}
-#endif
 
 }  // namespace uniserve

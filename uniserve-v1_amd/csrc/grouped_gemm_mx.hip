@@ -488,8 +488,13 @@ __global__ void __launch_bounds__(kWaves * kWave, 8 / kWaves) tiled_mx_kernel(Mx
       return r < rows ? first + r : first;
     }
   };
+  // The activation DMA's base: FC2's rows are the tile's own, addressed from the tile's first row,
+  // so their 32-bit lane offsets stay under 128 rows whatever the array's size; FC1's gathered
+  // token rows are addressed from the array, which the hosts hold below 4 GiB (dma_rows_fit).
+  const uint8_t *act_tile = p.act + (kGated ? 0 : first * p.K);
+  auto act_row = [&](int r) -> int64_t { return kGated ? source_row(r) : source_row(r) - first; };
 
-  // ---- DMA sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
+  // ---- DMA sources (32-bit lane offsets from wave-uniform bases) ----
   // Activations: wave w's instruction i fills tile rows 8 (kActLoads w + i) + l / 8, lane l
   // bringing logical chunk (l % 8) ^ key(row) into physical chunk l % 8; its scale instruction
   // brings the scale words of tile rows kActRows w + l % kActRows (the other lanes repeat them into
@@ -498,7 +503,7 @@ __global__ void __launch_bounds__(kWaves * kWave, 8 / kWaves) tiled_mx_kernel(Mx
 #pragma unroll
   for (int i = 0; i < kActLoads; ++i) {
     const int r = 8 * (kActLoads * wave + i) + lane / 8;
-    a_off[i] = static_cast<uint32_t>(source_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
+    a_off[i] = static_cast<uint32_t>(act_row(r) * p.K + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
   }
   const int as_r = kActRows * wave + lane % kActRows;
   const uint32_t as_off = static_cast<uint32_t>(
@@ -527,7 +532,7 @@ __global__ void __launch_bounds__(kWaves * kWave, 8 / kWaves) tiled_mx_kernel(Mx
     const uint32_t act_lds = lds_address(st.act + wave * kActLoads * kWave);
 #pragma unroll
     for (int i = 0; i < kActLoads; ++i)
-      dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+      dma16(act_tile + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
     const uint32_t weight_lds = lds_address(st.weights + wave * kWeightLoads * kWave);
 #pragma unroll
     for (int i = 0; i < kWeightLoads; ++i)
@@ -730,6 +735,9 @@ int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, 
       return UNISERVE_REFUSE(call, "gather_gemm_mx needs an intermediate width of whole 64-column slices");
     if (call->tokens < 0 || call->top <= 0 || call->experts <= 0)
       return UNISERVE_REFUSE(call, "gather_gemm_mx needs non-negative tokens and positive top and experts");
+    if (!dma_rows_fit(call->tokens, call->hidden_size))
+      return UNISERVE_REFUSE(call, "gather_gemm_mx serves hidden rows below 4 GiB (%lld tokens of %lld bytes)",
+                             static_cast<long long>(call->tokens), static_cast<long long>(call->hidden_size));
     if (call->permuted_rows < call->tokens * call->top || call->permuted_rows % kTileRows != 0)
       return UNISERVE_REFUSE(call, "gather_gemm_mx needs whole 128-row tiles that hold every route");
     if (call->weight_scale_layout != UNISERVE_MX_SCALES_ROW_MAJOR && call->weight_scale_layout != UNISERVE_MX_SCALES_STAGE_MAJOR)

@@ -36,20 +36,6 @@
 #include "grouped_fp8.hpp"
 #include "grouped_prefill.hpp"
 
-#ifdef UNISERVE_PAIR_TRACE
-// Development timing of each workgroup (s_memrealtime at its start, loop start, loop end and end;
-// HW_ID), read back by the trace entries of builds made with this macro only.
-static __device__ unsigned long long pair_trace[16384][8];
-#define UNISERVE_PAIR_MARK(slot)                                                                           \
-  do {                                                                                                     \
-    if (threadIdx.x == 0 && blockIdx.x < 16384) pair_trace[blockIdx.x][slot] = __builtin_amdgcn_s_memrealtime(); \
-  } while (0)
-#else
-#define UNISERVE_PAIR_MARK(slot) \
-  do {                           \
-  } while (0)
-#endif
-
 namespace uniserve {
 namespace pair {
 
@@ -158,7 +144,6 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   const int tile = first_tile + within % in_group;
   if (tile >= p.num_tiles[0]) return;
 
-  UNISERVE_PAIR_MARK(0);
   const int64_t expert = p.tile_to_expert[tile];
   const int64_t first = static_cast<int64_t>(tile) * kRows;
   const int rows = p.tile_to_limit[tile] - static_cast<int>(first);
@@ -180,8 +165,13 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
       return r < rows ? first + r : first;
     }
   };
+  // The activation DMA's base: FC2's rows are the tile's own, addressed from the tile's first row,
+  // so their 32-bit lane offsets stay under 128 rows whatever the array's size; FC1's gathered
+  // token rows are addressed from the array, which the hosts hold below 4 GiB (dma_rows_fit).
+  const uint8_t *act_tile = p.act + (kGated ? 0 : first * row_bytes);
+  auto act_row = [&](int r) -> int64_t { return kGated ? source_row(r) : source_row(r) - first; };
 
-  // ---- sources (32-bit lane offsets from wave-uniform bases; every array is below 4 GiB) ----
+  // ---- sources (32-bit lane offsets from wave-uniform bases) ----
   // Activations: wave w brings tile rows kActLoads * 8 w .., instruction i rows
   // kActLoads * 8 w + 8 i + l / 8, lane l the logical chunk (l % 8) ^ key(row) into physical
   // chunk l % 8.
@@ -189,7 +179,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
 #pragma unroll
   for (int i = 0; i < kActLoads; ++i) {
     const int r = kActLoads * 8 * wave + 8 * i + lane / 8;
-    a_off[i] = static_cast<uint32_t>(source_row(r) * row_bytes + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
+    a_off[i] = static_cast<uint32_t>(act_row(r) * row_bytes + ((lane & 7) ^ ((r >> 1) & 7)) * 16);
   }
   // Weights: the wave's 64 rows. FC1 rows 0..31 are up rows slice_col + 32 w .., rows 32..63 the
   // gate rows of the same columns; FC2 rows are 64 consecutive output columns. Instruction i
@@ -247,7 +237,7 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
 #pragma unroll
     for (int j = 0; j < kActLoads / 2; ++j) {
       const int i = h * (kActLoads / 2) + j;
-      dma16(p.act + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+      dma16(act_tile + static_cast<int64_t>(k) * 128, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
     }
   };
 
@@ -279,7 +269,6 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   issue_act(1, 0);
   issue_act(1, 1);
   if constexpr (F::kScaled) wait_loads_and_scales<kLast>(sx);
-  UNISERVE_PAIR_MARK(1);
   for (int k = 0; k < stages; ++k) {
     prefill::wait_loads_but<kLast>();
     __syncthreads();
@@ -364,7 +353,6 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
   }
   prefill::wait_all_loads();
   __syncthreads();  // every wave is done with the operand buffers
-  UNISERVE_PAIR_MARK(2);
 
   // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row 16 tb + r16
   // and the wave's weight rows 16 jb + 4 g + e in element e. The output tile goes through LDS so
@@ -473,7 +461,6 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
       const int64_t column = slice_col + group * 128 + sub * 8;
       *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(w, scale);
     }
-    UNISERVE_PAIR_MARK(3);
     return;
   }
   constexpr int kPieces = kOutCols / 8;
@@ -484,7 +471,6 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
     const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + c * 16);
     *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
   }
-  UNISERVE_PAIR_MARK(3);
 }
 
 }  // namespace pair

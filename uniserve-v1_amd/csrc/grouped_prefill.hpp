@@ -226,16 +226,21 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
       return r < rows ? first + r : first;
     }
   };
+  // The activation DMA's base: FC2's rows are the tile's own, addressed from the tile's first row,
+  // so their 32-bit lane offsets stay under 128 rows whatever the array's size; FC1's gathered
+  // token rows are addressed from the array, which the hosts hold below 4 GiB (dma_rows_fit).
+  const uint8_t *act_tile = p.act + (kGated ? 0 : first * row_bytes);
+  auto act_row = [&](int r) -> int64_t { return kGated ? source_row(r) : source_row(r) - first; };
 
   // ---- DMA sources: instruction i of this wave fills 8 whole LDS rows; lane l brings logical
   // chunk (l % 8) ^ key(row) of row 8 i' + l / 8, landing in physical chunk l % 8 ----
   // 32-bit lane offsets from wave-uniform bases keep the addresses in one VGPR each (the DMA's
-  // scalar-base form); every operand array here is below 4 GiB.
+  // scalar-base form).
   uint32_t a_off[kActLoads];
 #pragma unroll
   for (int i = 0; i < kActLoads; ++i) {
     const int r = (wave * kActLoads + i) * 8 + lane / 8;
-    const int64_t source = source_row(r);
+    const int64_t source = act_row(r);
     a_off[i] = static_cast<uint32_t>(source * row_bytes + ((lane & 7) ^ key(r)) * 16);
   }
   // This wave's 64 weight rows (LDS rows 64 w ..): FC1 rows 0..31 are up rows, 32..63 the gate
@@ -263,7 +268,7 @@ __global__ void __launch_bounds__(F::kWaves * kWave) prefill_kernel(PrefillParam
     const uint32_t act_lds = lds_address(st.act + wave * kActLoads * kWave);
 #pragma unroll
     for (int i = 0; i < kActLoads; ++i)
-      dma16(p.act + offset, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
+      dma16(act_tile + offset, a_off[i], __builtin_amdgcn_readfirstlane(act_lds + i * kWave * 16));
   };
   // `after_reads`: the wave's own weight rows of `st` were just read into registers; the first
   // DMA waits for those LDS reads (lgkmcnt 0) before it may overwrite them.

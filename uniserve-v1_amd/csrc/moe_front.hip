@@ -19,17 +19,6 @@
 //     every map entry the layer reads bit for bit the moe_sort entry's; the padding rows of the two
 //     permuted maps, which the layer never reads, are not written).
 // Each last taker resets its counter, so every launch leaves the counters zero.
-#ifdef UNISERVE_FRONT_TRACE
-#include <hip/hip_runtime.h>
-__device__ unsigned long long front_trace[64];
-#define UNISERVE_TRACE(slot)                                                                      \
-  do {                                                                                            \
-    if (threadIdx.x == 0) front_trace[slot] = __builtin_amdgcn_s_memrealtime();                   \
-  } while (0)
-extern "C" int uniserve_front_trace_read(unsigned long long *out) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(front_trace), sizeof(front_trace)) == hipSuccess ? 0 : 1;
-}
-#endif
 #include "common.hpp"
 #include "grouped_fp8.hpp"
 #include "grouped_mx.hpp"
@@ -46,26 +35,44 @@ constexpr int kUnroll = 4;                    // K steps of 32 whose loads a wav
 constexpr int kTile = 16;
 
 /// Takes a ticket of `counter` for one of `takers` workgroups; answers, to every thread, whether it
-/// was the last (then the counter is reset). What crosses workgroups - the scores and the ids - is
-/// stored and read at device scope, so a ticket needs no cache maintenance: every thread's stores
-/// have completed (vmcnt counts stores) before the workgroup's barrier and thread 0's count.
+/// was the last (then the counter is reset).
+///
+/// Ordering. What crosses workgroups - the scores and the ids - is stored and read only with
+/// relaxed agent-scope atomics (store_device / load_device). On gfx950 those are emitted with the
+/// sc1 bit: a store is written through the XCD's L2 to the memory-side coherence point and counts
+/// in vmcnt until that write is acknowledged there; a load bypasses the XCD's L2 and is served from
+/// the coherence point. So no L2 write-back (release) or invalidation (acquire) is needed - those
+/// exist for ordinary cached accesses, which this hand-off does not use. What remains is order:
+///   * publisher: every thread waits vmcnt(0) (its device-scope stores acknowledged), then the
+///     workgroup barrier, then thread 0's fetch_add - the ticket is taken only after every store of
+///     the workgroup has reached the coherence point;
+///   * taker: the ticket answer reaches the other threads through LDS behind a barrier, and their
+///     device-scope loads are issued after it.
+/// The language's memory model does not promise that order for relaxed atomics to different
+/// addresses, so it is pinned for the compiler with a full signal fence on each side of the
+/// ticket (no instruction emitted; no memory access moves across it), on top of the hardware
+/// wait. Release/acquire at agent scope would give the same order with an L2 write-back and
+/// invalidate per ticket; measured, the front end took 20.0 us that way against 17.8.
 __device__ __forceinline__ bool last_ticket(uint32_t *counter, uint32_t takers, int32_t *flag) {
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's device-scope stores acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const uint32_t taken = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = taken + 1 == takers;
     if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = last ? 1 : 0;
   }
   __syncthreads();
-  return *flag != 0;
+  const bool last = *flag != 0;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return last;
 }
 
 __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
   extern __shared__ __align__(16) int32_t front_lds[];
   __shared__ int32_t flag;
-  if (blockIdx.x == 0 && blockIdx.y == 0) UNISERVE_TRACE(0);
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int r16 = lane & 15;
@@ -170,7 +177,6 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
     quantize_share();
     return;
   }
-  UNISERVE_TRACE(1);
   const int half = static_cast<int>(threadIdx.x) / topk::kHalf;
   if (half < kTile) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kTile + half;
@@ -179,7 +185,6 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
                       p.renormalize, nullptr, -1, p.ids, p.weights, p.map, p.live, p.load, active);
   }
   __syncthreads();
-  UNISERVE_TRACE(2);
   if (!p.sort_routes) {
     // No sort: each route of the block is visible at its own expanded index, or not at all.
     const int64_t live = (p.live != nullptr ? static_cast<int64_t>(p.live[0]) : p.tokens) * p.top;
@@ -200,9 +205,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
     quantize_share();
     return;
   }
-  UNISERVE_TRACE(4);
   sort::small_sort<false, true>(p.sort, front_lds);
-  UNISERVE_TRACE(3);
   quantize_share();
 }
 

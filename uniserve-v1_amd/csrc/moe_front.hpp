@@ -9,6 +9,7 @@
 #include <cstdint>
 
 #include "sort_small.hpp"
+#include "uniserve_moe_unpermute.h"
 
 namespace uniserve {
 
@@ -50,5 +51,14 @@ struct FrontParams {
 bool front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top, int64_t local_experts);
 
 void launch_front(const FrontParams &p, hipStream_t stream);
+
+/// Counter words a launch over `tokens` tokens uses: the sort's and one per token block.
+inline int32_t front_ticket_words(int64_t tokens) { return static_cast<int32_t>(1 + (tokens + 15) / 16); }
+
+/// uniserve_moe_unpermute that also checks the front end's `ticket_words` counters at `ticket`
+/// (moe_unpermute.hip): nonzero words - counters that were not zero before the front end ran -
+/// turn the output into NaN and are cleared.
+int32_t moe_unpermute_checked(const uniserve_unpermute_call *call, uint32_t *ticket, int32_t ticket_words,
+                              void *stream);
 
 }  // namespace uniserve

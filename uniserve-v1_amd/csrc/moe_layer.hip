@@ -263,6 +263,9 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
                              static_cast<long long>(local_experts), static_cast<long long>(call->experts));
     if (call->tokens == 0) return 0;
     if (call->hidden_size % 64 != 0) return UNISERVE_REFUSE(call, "moe_layer needs a hidden size of whole 64-element steps");
+    if (!dma_rows_fit(call->tokens, call->hidden_size * 2))
+      return UNISERVE_REFUSE(call, "moe_layer serves hidden rows below 4 GiB (%lld tokens of %lld bytes)",
+                             static_cast<long long>(call->tokens), static_cast<long long>(call->hidden_size * 2));
     const int32_t activation = static_cast<int32_t>(call->activation);
     // Decode sizes: no sort - the fused front end routes, and the products' workgroups each serve
     // one local expert, finding its routes in `ids` (rows at expanded positions).
@@ -591,7 +594,12 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     combine.scales_dtype = UNISERVE_DTYPE_F32;
     combine.output_dtype = UNISERVE_DTYPE_BF16;
     combine.layout = by_expert ? UNISERVE_UNPERMUTE_LAYOUT_EXPANDED : UNISERVE_UNPERMUTE_LAYOUT_PERMUTED;
-    if (want(UNISERVE_MOE_LAYER_UNPERMUTE) && uniserve_moe_unpermute(&combine, stream) != 0) return forward_error(call, "moe_unpermute", combine);
+    // After the fused front end the combine also checks that the front end's counters came back to
+    // zero (they do unless they were not zero before it: a workspace whose head was not cleared).
+    uint32_t *ticket = front ? static_cast<uint32_t *>(at(v.ticket)) : nullptr;
+    if (want(UNISERVE_MOE_LAYER_UNPERMUTE) &&
+        moe_unpermute_checked(&combine, ticket, front ? front_ticket_words(call->tokens) : 0, stream) != 0)
+      return forward_error(call, "moe_unpermute", combine);
     return 0;
   });
 }
@@ -617,15 +625,19 @@ namespace {
 /// The layer's intermediates for callers that pass no workspace: one array per device, held from
 /// the library's load to the process's end. Host code never names it in a launch or a copy: the
 /// name is a host-side stand-in; the device address comes from hipGetSymbolAddress, per device.
+/// It has no initialiser, so it is zero-initialised storage (zero-filled when the code object is
+/// loaded on a device): the front end's ticket counters at its head start at zero, and every call
+/// leaves them zero. No memset is ever issued, so no call - the first one included - puts a memset
+/// node into a graph its caller is capturing.
 __device__ __align__(256) unsigned char scratch[UNISERVE_MOE_LAYER_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
 std::mutex scratch_mutex;
 void *scratch_address[kMaxDevices] = {};
 
-/// The device address of `scratch` on the current device, looked up once per device; its first
-/// word (the front end's counter, which every call leaves zero) is cleared on `stream` then.
-hipError_t scratch_of_current_device(void **address, hipStream_t stream) {
+/// The device address of `scratch` on the current device, looked up once per device (a host-side
+/// query: nothing is issued to any stream).
+hipError_t scratch_of_current_device(void **address) {
   int device = -1;
   hipError_t status = hipGetDevice(&device);
   if (status != hipSuccess) return status;
@@ -634,8 +646,6 @@ hipError_t scratch_of_current_device(void **address, hipStream_t stream) {
   if (scratch_address[device] == nullptr) {
     void *ptr = nullptr;
     status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (status != hipSuccess) return status;
-    status = hipMemsetAsync(ptr, 0, uniserve::kFrontTicketBytes, stream);
     if (status != hipSuccess) return status;
     scratch_address[device] = ptr;
   }
@@ -657,7 +667,7 @@ extern "C" int32_t uniserve_moe_layer_no_alloc(const uniserve_moe_layer_call *ca
                              "the library's %lld-byte scratch; pass a workspace to uniserve_moe_layer instead",
                              static_cast<long long>(v.total), static_cast<long long>(UNISERVE_MOE_LAYER_SCRATCH_BYTES));
     void *address = nullptr;
-    const hipError_t status = scratch_of_current_device(&address, static_cast<hipStream_t>(stream));
+    const hipError_t status = scratch_of_current_device(&address);
     if (status != hipSuccess)
       return UNISERVE_REFUSE(call, "moe_layer_no_alloc: no scratch address on this device: %s", hipGetErrorString(status));
     return run_layer(call, -1, stream, address, UNISERVE_MOE_LAYER_SCRATCH_BYTES);

@@ -9,6 +9,7 @@
 // is negative (or names no row of `routes`) contributes nothing, so a token with no visible route is
 // exactly zero. HBM-bound: each lane moves 16 bytes (8 elements) of every route row of its token.
 #include "common.hpp"
+#include "moe_front.hpp"
 #include "uniserve_moe_unpermute.h"
 
 namespace uniserve {
@@ -29,6 +30,13 @@ struct CombineParams {
   int64_t hidden;
   int64_t routes_rows;
   int32_t expanded;
+  // Inside the MoE layer after its fused decode front end: the front end's ticket counters, which
+  // a correct launch leaves zero (null elsewhere). A nonzero word means the workspace's counters
+  // were not zero before the front end ran - then its routing may have run before every score was
+  // stored - so the combine writes NaN in place of the output and clears the words, so that the
+  // next call routes correctly.
+  uint32_t *ticket;
+  int32_t ticket_words;
 };
 
 template <class Element>
@@ -52,9 +60,13 @@ template <class Element, class Scale>
 __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams p) {
   const int64_t token = blockIdx.x;
   const int64_t column = static_cast<int64_t>(blockIdx.y) * kColumnsPerBlock + threadIdx.x * kPerLane;
-  if (column >= p.hidden) return;
+  const bool in_range = column < p.hidden;
+  if (!in_range && p.ticket == nullptr) return;  // with a ticket check every lane meets the barrier
   const Element *routes = static_cast<const Element *>(p.routes);
   const Scale *scales = static_cast<const Scale *>(p.scales);
+  // Issued first, used last: the counter check costs no round trip of its own.
+  const uint32_t ticket_word =
+      p.ticket != nullptr && static_cast<int>(threadIdx.x) < p.ticket_words ? load_device(p.ticket + threadIdx.x) : 0u;
   float sum[kPerLane];
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) sum[j] = 0.0f;
@@ -79,7 +91,7 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
       // invisible route's row read and then ignored.
       const bool visible = p.expanded ? k0 + u < p.top : entry[u] >= 0 && entry[u] < p.routes_rows;
       const int64_t row = p.expanded ? token * p.top + k0 + u : entry[u];
-      if (visible) {
+      if (visible && in_range) {
         const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(routes + row * p.hidden + column));
         packed[u] = uint4{v[0], v[1], v[2], v[3]};
       } else {
@@ -94,18 +106,24 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
       for (int j = 0; j < kPerLane; ++j) sum[j] = __builtin_fmaf(weight[u], widen<Element>(values[j]), sum[j]);
     }
   }
+  if (p.ticket != nullptr && __syncthreads_or(ticket_word != 0u)) {
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) sum[j] = __builtin_nanf("");
+    if (blockIdx.x == 0 && blockIdx.y == 0 && static_cast<int>(threadIdx.x) < p.ticket_words)
+      store_device(p.ticket + threadIdx.x, 0u);
+  }
   Element result[kPerLane];
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) result[j] = narrow<Element>(sum[j]);
-  *reinterpret_cast<uint4 *>(static_cast<Element *>(p.out) + token * p.hidden + column) =
-      *reinterpret_cast<const uint4 *>(result);
+  if (in_range)
+    *reinterpret_cast<uint4 *>(static_cast<Element *>(p.out) + token * p.hidden + column) =
+        *reinterpret_cast<const uint4 *>(result);
 }
 
 }  // namespace
-}  // namespace uniserve
 
-extern "C" int32_t uniserve_moe_unpermute(const uniserve_unpermute_call *call, void *stream) {
-  using namespace uniserve;
+int32_t moe_unpermute_checked(const uniserve_unpermute_call *call, uint32_t *ticket, int32_t ticket_words,
+                              void *stream) {
   return guarded(call, [&]() -> int32_t {
     if (call->input_dtype != call->output_dtype)
       return UNISERVE_REFUSE(call, "moe_unpermute needs one input and output dtype");
@@ -126,7 +144,9 @@ extern "C" int32_t uniserve_moe_unpermute(const uniserve_unpermute_call *call, v
 
     CombineParams p{call->routes, call->out, call->expanded_to_permuted, call->scales,
                     call->top,    call->hidden, call->routes_rows,
-                    call->layout == UNISERVE_UNPERMUTE_LAYOUT_EXPANDED ? 1 : 0};
+                    call->layout == UNISERVE_UNPERMUTE_LAYOUT_EXPANDED ? 1 : 0, ticket, ticket_words};
+    if (ticket != nullptr && (ticket_words < 1 || ticket_words > kCombineThreads))
+      return UNISERVE_REFUSE(call, "moe_unpermute: %d ticket words to check", ticket_words);
     const dim3 grid(static_cast<uint32_t>(call->tokens),
                     static_cast<uint32_t>(ceil_div<int64_t>(call->hidden, kColumnsPerBlock)));
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -149,4 +169,10 @@ extern "C" int32_t uniserve_moe_unpermute(const uniserve_unpermute_call *call, v
     }
     return launched(call, "moe_unpermute");
   });
+}
+
+}  // namespace uniserve
+
+extern "C" int32_t uniserve_moe_unpermute(const uniserve_unpermute_call *call, void *stream) {
+  return uniserve::moe_unpermute_checked(call, nullptr, 0, stream);
 }
