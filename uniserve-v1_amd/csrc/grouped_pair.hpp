@@ -352,17 +352,66 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
     }
   }
   prefill::wait_all_loads();
-  __syncthreads();  // every wave is done with the operand buffers
-
-  // ---- epilogue: lane (r16, g) holds, of token block tb and weight block jb, tile row 16 tb + r16
-  // and the wave's weight rows 16 jb + 4 g + e in element e. The output tile goes through LDS so
-  // the global stores are whole rows. ----
-  constexpr int kOutCols = kGated ? kSliceRows / 2 : kSliceRows;
-  constexpr int kOutStride = out_stride<kGated>();
+  if (!(kGated && p.out_codes != nullptr)) {
+    // Each wave stages its own columns of one token block at a time in its own weight buffer (no
+    // other wave reads it, and its last loads have landed), then stores whole 16-byte pieces.
+    constexpr int kWaveCols = kGated ? kWaveRows / 2 : kWaveRows;  // bf16 columns of this wave
+    constexpr int kRowBytes = kWaveCols * 2;
+    constexpr int kStride = kRowBytes + 16;
+    constexpr int kPiecesPerRow = kRowBytes / 16;
+    char *stage = reinterpret_cast<char *>(sh.weights[wave]);
+    uint16_t *out_cols = p.out + slice_col + wave * kWaveCols;
 #pragma unroll
-  for (int tb = 0; tb < kTokenBlocks; ++tb) {
-    char *row = lds + (tb * 16 + r16) * kOutStride;
-    if constexpr (kGated) {
+    for (int tb = 0; tb < kTokenBlocks; ++tb) {
+      char *row = stage + r16 * kStride;
+      if constexpr (kGated) {
+        auto gated = [&](auto activation) {
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gate_of<decltype(activation)::value>(acc[tb][jb + 2][e]) * acc[tb][jb][e];
+            uint2 packed;
+            packed.x = pack_bf16x2(v[0], v[1]);
+            packed.y = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<uint2 *>(row + (jb * 16 + 4 * g) * 2) = packed;
+          }
+        };
+        if (p.activation == UNISERVE_ACTIVATION_GELU_TANH) gated(std::integral_constant<int, UNISERVE_ACTIVATION_GELU_TANH>{});
+        else gated(std::integral_constant<int, UNISERVE_ACTIVATION_SILU>{});
+      } else {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          uint2 packed;
+          packed.x = pack_bf16x2(acc[tb][jb][0], acc[tb][jb][1]);
+          packed.y = pack_bf16x2(acc[tb][jb][2], acc[tb][jb][3]);
+          *reinterpret_cast<uint2 *>(row + (jb * 16 + 4 * g) * 2) = packed;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int piece = lane; piece < 16 * kPiecesPerRow; piece += kWave) {
+        const int r = piece / kPiecesPerRow;
+        const int c = piece - r * kPiecesPerRow;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * kStride + c * 16);
+        const int m = tb * 16 + r;
+        if (m < rows) *reinterpret_cast<u32x4 *>(out_cols + (first + m) * p.out_width + c * 8) = v;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    return;
+  }
+  if constexpr (kGated) {
+    __syncthreads();  // every wave is done with the operand buffers
+
+    // ---- e4m3 FC1 written as FC2's operand: lane (r16, g) holds, of token block tb and weight
+    // block jb, tile row 16 tb + r16 and the wave's weight rows 16 jb + 4 g + e in element e. The
+    // gated bf16 tile goes through LDS, where 16 lanes take each (row, 128-column group). ----
+    constexpr int kOutCols = kSliceRows / 2;
+    constexpr int kOutStride = out_stride<kGated>();
+#pragma unroll
+    for (int tb = 0; tb < kTokenBlocks; ++tb) {
+      char *row = lds + (tb * 16 + r16) * kOutStride;
       // The activation is uniform over the launch: one branch, each side with its gate inlined.
       auto gated = [&](auto activation) {
 #pragma unroll
@@ -378,18 +427,8 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
       };
       if (p.activation == UNISERVE_ACTIVATION_GELU_TANH) gated(std::integral_constant<int, UNISERVE_ACTIVATION_GELU_TANH>{});
       else gated(std::integral_constant<int, UNISERVE_ACTIVATION_SILU>{});
-    } else {
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        uint2 packed;
-        packed.x = pack_bf16x2(acc[tb][jb][0], acc[tb][jb][1]);
-        packed.y = pack_bf16x2(acc[tb][jb][2], acc[tb][jb][3]);
-        *reinterpret_cast<uint2 *>(row + (wave * 64 + jb * 16 + 4 * g) * 2) = packed;
-      }
     }
-  }
-  __syncthreads();
-  if (kGated && p.out_codes != nullptr) {
+    __syncthreads();
     // Written as the FC2 operand: each (row, 128-column group) quantised by 16 lanes (one DPP
     // row) from the bf16 values (the stand-alone quantiser's rounding points and encoding: amax of
     // the bf16 values, s = amax / 448, code = e4m3(v / s)); live rows only. Every lane's passes
@@ -461,15 +500,6 @@ __global__ void __launch_bounds__(kThreads, 2) pair_kernel(PrefillParams p) {
       const int64_t column = slice_col + group * 128 + sub * 8;
       *reinterpret_cast<uint2 *>(p.out_codes + (first + m) * p.out_width + column) = e4m3_eight(w, scale);
     }
-    return;
-  }
-  constexpr int kPieces = kOutCols / 8;
-  for (int index = t; index < kRows * kPieces; index += kThreads) {
-    const int m = index / kPieces;
-    const int c = index - m * kPieces;
-    if (m >= rows) continue;
-    const u32x4 piece = *reinterpret_cast<const u32x4 *>(lds + m * kOutStride + c * 16);
-    *reinterpret_cast<u32x4 *>(p.out + (first + m) * p.out_width + slice_col + c * 8) = piece;
   }
 }
 
