@@ -249,3 +249,26 @@ def test_uncleared_front_counters_fail_loudly_then_clear(device, garbage):
     announce("front counters: the call after", garbage)
     again = bf16_bits(layer(x, router, up_gate, down))
     assert np.array_equal(again, clean)
+
+
+@pytest.mark.parametrize("wdtype", ["bf16", "f8e4m3", "f4e2m1"])
+def test_prefill_layer_reads_nothing_it_did_not_write(device, wdtype):
+    """A prefill-size layer over a workspace whose bytes are all 0x01 (but the front end's counter
+    words, which must start at zero) gives the zero workspace's output bit for bit: every
+    intermediate is written before it is read, so a reused buffer (the no-alloc scratch, a pool)
+    behaves like a fresh one. 0x01 bytes make any unwritten index read a large one."""
+    tokens, hidden, experts, top, intermediate = 1024, 2048, 128, 8, 768
+    announce("prefill layer over a dirty workspace", wdtype)
+    x = normal_bf16((tokens, hidden), 81, device=device)
+    router = normal_bf16((experts, hidden), 82, 0.02, device)
+    up_gate_bf16 = normal_bf16((experts, 2 * intermediate, hidden), 83, 0.02, device)
+    down_bf16 = normal_bf16((experts, hidden, intermediate), 84, 0.02, device)
+    _, _, _, _, up_gate, down, kw = quantised(wdtype, up_gate_bf16, down_bf16, device)
+    outs = []
+    for dirty in (False, True):
+        layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+        if dirty:
+            layer.workspace.fill_(1)
+            layer.workspace[:1024].zero_()
+        outs.append(bf16_bits(layer(x, router, up_gate, down, **kw)).copy())
+    np.testing.assert_array_equal(outs[1], outs[0])

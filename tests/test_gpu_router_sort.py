@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle_lib as O
-from gpu_helpers import announce, bf16_bits, to_bf16, zipf_bias
+from gpu_helpers import announce, bf16_bits, bf16_values, to_bf16, zipf_bias
 from uniserve_moe import ops
 
 pytestmark = pytest.mark.gpu
@@ -205,3 +205,118 @@ def test_sort_of_a_window_with_out_of_range_ids(device):
     ids = rng.integers(-3, 140, (5000, 8)).astype(np.int32)  # ids outside the vocabulary are not held
     got, want = sort_both(device, ids, 140, (20, 100), 4900)
     assert_sort_equal(got, want, 5000, 8)
+
+
+PREFILL_FRONT = {
+    # name: tokens, hidden, experts, top, weights, zipf, window, live, map
+    "bf16 30B 8192 zipf": (8192, 2048, 128, 8, "bf16", True, None, None, False),
+    "fp8 30B 2048, map + load + live": (2048, 2048, 128, 8, "f8e4m3", False, None, 2000, True),
+    "fp8 235B 4096 zipf": (4096, 4096, 128, 8, "f8e4m3", True, None, None, False),
+    "mx 30B 2048 window": (2048, 2048, 128, 8, "f4e2m1", False, (8, 112), None, False),
+    "bf16 60 experts, 2000 tokens": (2000, 256, 60, 4, "bf16", False, None, 1999, True),
+}
+
+
+@pytest.mark.parametrize("case", list(PREFILL_FRONT))
+def test_prefill_front_is_the_separate_operators(device, case):
+    """At prefill sizes the layer computes the router scores, topk_softmax and (e4m3, MXFP4) the
+    hidden rows' quantisation in one launch. Against the separate operators on the same inputs:
+    the scores are the oracle's router within one bf16 step (>= 99% bit for bit: FP32 sums in
+    another order), and, given the layer's own scores, the ids, weights and expert load are the
+    topk_softmax entry's bit for bit, the seven maps the moe_sort entry's, the hidden codes and
+    scales the stand-alone quantiser's, and every held route's row of the route-major scale table
+    its token's scales."""
+    tokens, hidden, experts, top, wdtype, zipf, window, live, with_map = PREFILL_FRONT[case]
+    announce("prefill front", case)
+    intermediate = 256
+    g = torch.Generator(device=device).manual_seed(17)
+    x = (torch.randn((tokens, hidden), generator=g, device=device)).to(torch.bfloat16)
+    router = (torch.randn((experts, hidden), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    bias = torch.from_numpy(zipf_bias(experts)).to(device) if zipf else None
+    local_experts = experts if window is None else window[1]
+    up_gate = (torch.randn((local_experts, 2 * intermediate, hidden), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    down = (torch.randn((local_experts, hidden, intermediate), generator=g, device=device) * 0.02).to(torch.bfloat16)
+    kw = {}
+    if wdtype == "f8e4m3":
+        q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+    elif wdtype == "f4e2m1":
+        q1, s1 = O.quantize_blocks_mxfp4(bf16_bits(up_gate))
+        q2, s2 = O.quantize_blocks_mxfp4(bf16_bits(down))
+    if wdtype != "bf16":
+        d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+        up_gate, down = d(q1), d(q2)
+        kw = dict(up_gate_scales=d(s1), down_scales=d(s2))
+    rng = np.random.default_rng(5)
+    mapping = torch.from_numpy(rng.permutation(experts).astype(np.int32)).to(device) if with_map else None
+    load = torch.zeros(experts, dtype=torch.int64, device=device)
+    live_t = None if live is None else torch.tensor([live], dtype=torch.int32, device=device)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype=wdtype)
+    layer(x, router, up_gate, down, router_bias=bias, live_tokens=live_t, mapping=mapping, load=load, window=window,
+          **kw)
+    torch.cuda.synchronize()
+
+    scores = layer.view("scores", torch.bfloat16, (tokens, experts)).clone()
+    want_scores = O.router_gemm(bf16_bits(x), bf16_bits(router), None if bias is None else zipf_bias(experts))
+    got_bits = bf16_bits(scores)
+    assert (got_bits == want_scores).mean() > 0.99
+    # Each side's FP32 sum is within n u sum|x w| of the exact one, then rounded once to bf16.
+    magnitude = np.abs(bf16_values(x)) @ np.abs(bf16_values(router)).T
+    want_values = O.bf16_decode(want_scores).astype(np.float64)
+    bound = 2.0**-7 * np.abs(want_values) + 2.0 * hidden * 2.0**-24 * magnitude
+    assert (np.abs(bf16_values(scores) - want_values) <= bound).all()
+
+    want_load = torch.zeros(experts, dtype=torch.int64, device=device)
+    want_ids, want_weights = ops.topk_softmax(scores, top, True, None, mapping, live_t, want_load)
+    ids = layer.view("ids", torch.int32, (tokens, top))
+    weights = layer.view("weights", torch.float32, (tokens, top))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), want_ids.cpu().numpy())
+    np.testing.assert_array_equal(weights.cpu().numpy().view(np.uint32), want_weights.cpu().numpy().view(np.uint32))
+    np.testing.assert_array_equal(load.cpu().numpy(), want_load.cpu().numpy())
+
+    maps = ops.moe_sort(ids, weights, experts, local=None if window is None else (window[0], window[0] + window[1]),
+                        live_tokens=live_t)
+    torch.cuda.synchronize()
+    rows = layer.views.permuted_rows
+    lengths = {"tile_to_expert": layer.views.max_tiles, "tile_to_limit": layer.views.max_tiles,
+               "expanded_to_permuted": tokens * top, "permuted_to_expanded": rows, "permuted_to_token": rows,
+               "total_padded_tokens": 1, "num_non_exiting_tiles": 1}
+    padded = int(maps[5][0].item())
+    for index, name in enumerate(lengths):
+        got = layer.view(name, torch.int32, (lengths[name],)).cpu().numpy()
+        want = maps[index][:lengths[name]].cpu().numpy()
+        if name in ("permuted_to_expanded", "permuted_to_token"):
+            got, want = got[:padded], want[:padded]
+        if name in ("tile_to_expert", "tile_to_limit"):
+            live_tiles = int(maps[6][0].item())
+            got, want = got[:live_tiles], want[:live_tiles]
+        np.testing.assert_array_equal(got, want, err_msg=name)
+
+    if wdtype == "bf16":
+        return
+    quantise = ops.quantize_fp8 if wdtype == "f8e4m3" else ops.quantize_mxfp8
+    want_q, want_s = quantise(x)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(layer.view("hidden_q", torch.uint8, (tokens, hidden)).cpu().numpy(),
+                                  want_q.cpu().numpy())
+    e2p = layer.view("expanded_to_permuted", torch.int32, (tokens * top,)).cpu().numpy()
+    held = np.nonzero(e2p >= 0)[0]
+    token_of = held // top
+    words = hidden // 128
+    if wdtype == "f8e4m3":
+        token_words = want_s.cpu().numpy().view(np.uint32)  # [tokens, hidden / 128]
+        if layer.views.route_scales:
+            table = layer.view("hidden_route_s", torch.float32, (words, rows)).cpu().numpy().view(np.uint32).T
+            np.testing.assert_array_equal(table[e2p[held]], token_words[token_of])
+        else:
+            np.testing.assert_array_equal(
+                layer.view("hidden_s", torch.float32, (tokens, words)).cpu().numpy().view(np.uint32), token_words)
+    else:
+        token_words = np.ascontiguousarray(want_s.cpu().numpy()).view(np.uint32).reshape(tokens, words)
+        if layer.views.route_scales:
+            table = layer.view("hidden_s", torch.int32, (words, rows)).cpu().numpy().view(np.uint32).T
+            np.testing.assert_array_equal(table[e2p[held]], token_words[token_of])
+        else:
+            np.testing.assert_array_equal(
+                layer.view("hidden_s", torch.uint8, (tokens, hidden // 32)).cpu().numpy(), want_s.cpu().numpy())

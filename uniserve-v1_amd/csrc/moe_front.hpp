@@ -52,6 +52,40 @@ bool front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top, in
 
 void launch_front(const FrontParams &p, hipStream_t stream);
 
+/// The front end at prefill sizes (front_prefill.hip): router scores, topk and (with `codes`) the
+/// hidden rows' quantisation in one launch, one workgroup per 32 tokens.
+struct PrefillFrontParams {
+  const uint16_t *x;        ///< [tokens, hidden] bf16
+  const uint16_t *w;        ///< [experts, hidden] bf16 router
+  const float *bias;        ///< [experts] or null
+  uint16_t *scores;         ///< [tokens, experts] bf16
+  int64_t tokens, experts, hidden;
+  int32_t top, renormalize;
+  const int32_t *map;       ///< [experts] or null
+  const int32_t *live;      ///< [1] or null
+  unsigned long long *load; ///< [experts] or null
+  int32_t *ids;             ///< [tokens, top]
+  float *weights;           ///< [tokens, top]
+  /// Or null: the hidden rows as e4m3 codes [tokens, hidden] with FP32 scales [tokens, hidden / 128]
+  /// (`scales`), or as MXFP8 codes with E8M0 bytes [tokens, hidden / 32] (`mx_scales`).
+  uint8_t *codes;
+  float *scales;
+  uint8_t *mx_scales;
+};
+
+/// Whether one launch serves these extents: at most 128 experts picking at most 32, whole
+/// 128-channel stages.
+bool prefill_front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top);
+
+void launch_prefill_front(const PrefillFrontParams &p, hipStream_t stream);
+
+/// Each route's copy of its token's `words` 4-byte scale words: token-major `from` ([tokens,
+/// words]) to route-major `to` ([words, rows] by permuted row), for the rows below the sort's
+/// total_padded_tokens (`padded`, on the device) whose permuted_to_expanded names a route; padding
+/// rows and rows past them are left alone.
+void launch_scatter_route_words(const uint32_t *from, const int32_t *permuted_to_expanded, const int32_t *padded,
+                                uint32_t *to, int64_t rows, int64_t top, int64_t words, hipStream_t stream);
+
 /// Counter words a launch over `tokens` tokens uses: the sort's and one per token block.
 inline int32_t front_ticket_words(int64_t tokens) { return static_cast<int32_t>(1 + (tokens + 15) / 16); }
 

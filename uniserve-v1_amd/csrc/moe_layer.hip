@@ -115,12 +115,38 @@ extern "C" int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_s
 
 namespace {
 
+/// moe_sort over the window's experts, as the layer calls it.
+int32_t run_sort(const uniserve_moe_layer_call *call, int32_t *ids, float *weights, int32_t *t2e, int32_t *t2l,
+                 int32_t *e2p, int32_t *p2e, int32_t *p2t, int32_t *padded, int32_t *tiles, int64_t local_experts,
+                 void *stream) {
+  uniserve_moe_sort_call sort{};
+  sort.ids = ids;
+  sort.scales = weights;
+  sort.tile_to_expert = t2e;
+  sort.tile_to_limit = t2l;
+  sort.expanded_to_permuted = e2p;
+  sort.permuted_to_expanded = p2e;
+  sort.total_padded_tokens = padded;
+  sort.num_non_exiting_tiles = tiles;
+  sort.tokens = call->tokens;
+  sort.top = call->top;
+  sort.experts = call->experts;
+  sort.local_experts = local_experts;
+  sort.local_offset = call->local_offset;
+  sort.tile_tokens = kTile;
+  sort.scales_dtype = UNISERVE_DTYPE_F32;
+  sort.live_tokens = call->live_tokens;
+  sort.permuted_to_token = p2t;
+  if (uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
+  return 0;
+}
+
 /// MXFP4 experts: quantise the hidden rows to MXFP8, FC1, quantise the live gated rows, FC2.
 /// `by_expert` set: the decode products without a sort (rows at expanded positions).
 template <class Want>
 int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_layer_views &v, char *ws,
                         const Want &want, void *stream, const uniserve::ExpertRouting *by_expert,
-                        bool hidden_quantised) {
+                        bool hidden_quantised, bool token_scales_waiting) {
   using namespace uniserve;
   auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
   const auto *t2e = static_cast<const int32_t *>(at(v.tile_to_expert));
@@ -137,7 +163,15 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   qx.rows = call->tokens;
   qx.width = call->hidden_size;
   qx.input_dtype = UNISERVE_DTYPE_BF16;
-  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || hidden_quantised) {
+  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || (hidden_quantised && !token_scales_waiting)) {
+  } else if (hidden_quantised) {
+    // The prefill front end quantised the rows; its token-major scale bytes (parked in the
+    // products' rows) go to the routes' rows, one 4-byte word per 128-channel stage.
+    launch_scatter_route_words(static_cast<const uint32_t *>(at(v.products)), p2e,
+                               static_cast<const int32_t *>(at(v.total_padded_tokens)),
+                               static_cast<uint32_t *>(at(v.hidden_s)), scale_rows, call->top,
+                               call->hidden_size / 128, s);
+    if (int32_t status = launched(call, "scatter of the hidden scales")) return status;
   } else if (scale_rows != 0) {
     // Each token's scale words go to its routes' permuted rows.
     launch_quantize_mxfp8(call->hidden, false, static_cast<uint8_t *>(at(v.hidden_q)), nullptr, nullptr, call->tokens,
@@ -279,6 +313,13 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     // e4m3 and MXFP4 at those sizes: the front end also quantises the hidden rows (QUANTIZE_HIDDEN
     // then launches nothing).
     const bool front_quantizes = front && (fp8 || mx) && !v.route_scales && call->hidden_size % 128 == 0;
+    // Prefill sizes: router scores, topk and (e4m3, MXFP4) the hidden rows' quantisation in one
+    // launch (ROUTER; TOPK launches nothing). The scales come out token-major; where the products
+    // take them route-major, QUANTIZE_HIDDEN copies each token's scales to its routes' rows once
+    // the sort has placed them.
+    const bool prefill_front =
+        !front && prefill_front_fits(call->tokens, call->experts, call->hidden_size, call->top);
+    const bool prefill_quantizes = prefill_front && (fp8 || mx);
 
     char *ws = static_cast<char *>(workspace);
     auto at = [&](int64_t offset) { return static_cast<void *>(ws + offset); };
@@ -340,6 +381,39 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         launch_front(fp, s);
         if (int32_t status = launched(call, "router, topk and sort")) return status;
       }
+    } else if (prefill_front) {
+      if (want(UNISERVE_MOE_LAYER_ROUTER)) {
+        PrefillFrontParams pp{};
+        pp.x = static_cast<const uint16_t *>(call->hidden);
+        pp.w = static_cast<const uint16_t *>(call->router);
+        pp.bias = call->router_bias;
+        pp.scores = static_cast<uint16_t *>(at(v.scores));
+        pp.tokens = call->tokens;
+        pp.experts = call->experts;
+        pp.hidden = call->hidden_size;
+        pp.top = static_cast<int32_t>(call->top);
+        pp.renormalize = call->renormalize ? 1 : 0;
+        pp.map = call->map;
+        pp.live = call->live_tokens;
+        pp.load = reinterpret_cast<unsigned long long *>(call->load);
+        pp.ids = ids;
+        pp.weights = weights;
+        if (fp8) {
+          pp.codes = static_cast<uint8_t *>(at(v.hidden_q));
+          pp.scales = static_cast<float *>(at(v.hidden_s));
+        } else if (mx) {
+          // Route-major MX scales: the token-major bytes wait in the products' rows (written only
+          // by FC2, later) until QUANTIZE_HIDDEN copies them to the routes' rows.
+          pp.codes = static_cast<uint8_t *>(at(v.hidden_q));
+          pp.mx_scales = static_cast<uint8_t *>(at(v.route_scales ? v.products : v.hidden_s));
+        }
+        launch_prefill_front(pp, s);
+        if (int32_t status = launched(call, "router and topk")) return status;
+      }
+      if (want(UNISERVE_MOE_LAYER_SORT)) {
+        if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, stream))
+          return status;
+      }
     } else {
     // 1. Router scores, bf16 (the router Linear's output dtype).
     RouterParams rp{static_cast<const uint16_t *>(call->hidden), static_cast<const uint16_t *>(call->router),
@@ -361,31 +435,17 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       return UNISERVE_REFUSE(call, "topk_softmax: %s", message);
 
     // 3. moe_sort over the window's experts.
-    uniserve_moe_sort_call sort{};
-    sort.ids = ids;
-    sort.scales = weights;
-    sort.tile_to_expert = t2e;
-    sort.tile_to_limit = t2l;
-    sort.expanded_to_permuted = e2p;
-    sort.permuted_to_expanded = p2e;
-    sort.total_padded_tokens = padded;
-    sort.num_non_exiting_tiles = tiles;
-    sort.tokens = call->tokens;
-    sort.top = call->top;
-    sort.experts = call->experts;
-    sort.local_experts = local_experts;
-    sort.local_offset = call->local_offset;
-    sort.tile_tokens = kTile;
-    sort.scales_dtype = UNISERVE_DTYPE_F32;
-    sort.live_tokens = call->live_tokens;
-    sort.permuted_to_token = p2t;
-    if (want(UNISERVE_MOE_LAYER_SORT) && uniserve_moe_sort(&sort, stream) != 0) return forward_error(call, "moe_sort", sort);
+    if (want(UNISERVE_MOE_LAYER_SORT)) {
+      if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, stream))
+        return status;
+    }
     }
 
     // 4-5. The two products.
     if (mx) {
       const ExpertRouting routing{ids, call->live_tokens, routes, call->top, call->local_offset, local_experts};
-      if (int32_t status = run_mx_products(call, v, ws, want, stream, by_expert ? &routing : nullptr, front_quantizes))
+      if (int32_t status = run_mx_products(call, v, ws, want, stream, by_expert ? &routing : nullptr,
+                                                 front_quantizes || prefill_quantizes, prefill_quantizes && v.route_scales))
         return status;
     } else if (by_expert && !fp8) {
       ExpertStream e{};
@@ -464,7 +524,13 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       qx.width = call->hidden_size;
       qx.input_dtype = UNISERVE_DTYPE_BF16;
       qx.group = 128;
-      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || front_quantizes) {
+      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || front_quantizes || (prefill_quantizes && scale_rows == 0)) {
+      } else if (prefill_quantizes) {
+        // The prefill front end quantised the rows; each token's scales go to its routes' rows.
+        launch_scatter_route_words(static_cast<const uint32_t *>(at(v.hidden_s)), p2e, padded,
+                                   static_cast<uint32_t *>(at(v.hidden_route_s)), scale_rows, call->top,
+                                   call->hidden_size / 128, s);
+        if (int32_t status = launched(call, "scatter of the hidden scales")) return status;
       } else if (scale_rows != 0) {
         launch_quantize_fp8_routes(static_cast<const uint16_t *>(call->hidden), static_cast<uint8_t *>(at(v.hidden_q)),
                                    static_cast<float *>(at(v.hidden_s)), static_cast<float *>(at(v.hidden_route_s)), e2p,

@@ -123,13 +123,13 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
                                       int row, int experts, int top, int renormalize,
                                       const void *scale, int scale_kind, int32_t *ids,
                                       float *weights, const int32_t *map, const int32_t *live,
-                                      unsigned long long *load, bool active) {
+                                      unsigned long long *load, bool active, int score_row) {
   const int lane = static_cast<int>(threadIdx.x) & (kHalf - 1);
   float values[kIter];
 #pragma unroll
   for (int it = 0; it < kIter; ++it) {
     const int expert = lane + it * kHalf;
-    const int64_t at = static_cast<int64_t>(row) * row_stride + expert;
+    const int64_t at = static_cast<int64_t>(score_row) * row_stride + expert;
     values[it] = expert < experts ? (kDevice ? load_kind_device(scores, score_kind, at) : load_kind(scores, score_kind, at))
                                   : -__builtin_inff();
   }
@@ -224,25 +224,28 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
 
 
 /// Routes token `row` (`active` false: take part in the wavefront's exchanges, store nothing),
-/// with the per-lane slot count the expert count needs.
+/// with the per-lane slot count the expert count needs; its scores are row `score_row` of
+/// `scores` (-1: row `row`).
 template <bool kDevice = false>
 __device__ __forceinline__ void route_token(const void *scores, int score_kind, int64_t row_stride, int row,
                                             int experts, int top, int renormalize, const void *scale,
                                             int scale_kind, int32_t *ids, float *weights, const int32_t *map,
-                                            const int32_t *live, unsigned long long *load, bool active) {
+                                            const int32_t *live, unsigned long long *load, bool active,
+                                            int score_row = -1) {
+  if (score_row < 0) score_row = row;
   const int needed = (experts + kHalf - 1) / kHalf;
   if (needed <= 1)
-    route<1, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<1, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active, score_row);
   else if (needed <= 2)
-    route<2, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<2, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active, score_row);
   else if (needed <= 4)
-    route<4, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<4, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active, score_row);
   else if (needed <= 8)
-    route<8, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<8, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active, score_row);
   else if (needed <= 16)
-    route<16, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<16, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active, score_row);
   else
-    route<32, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active);
+    route<32, kDevice>(scores, score_kind, row_stride, row, experts, top, renormalize, scale, scale_kind, ids, weights, map, live, load, active, score_row);
 }
 
 }  // namespace topk
