@@ -52,6 +52,12 @@ bool front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top, in
 
 void launch_front(const FrontParams &p, hipStream_t stream);
 
+/// The same front end where the layer skips the sort (sort_routes 0), one workgroup per token and
+/// no hand-off between workgroups: at least 32 tokens, at most 128 experts, the hidden size in
+/// whole 512-channel chunks up to 4096.
+bool local_front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top);
+void launch_local_front(const FrontParams &p, hipStream_t stream);
+
 /// The front end at prefill sizes (front_prefill.hip): router scores, topk and (with `codes`) the
 /// hidden rows' quantisation in one launch, one workgroup per 32 tokens.
 struct PrefillFrontParams {

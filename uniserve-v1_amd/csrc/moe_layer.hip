@@ -378,7 +378,10 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
           if (mx) fp.hidden_mx_scales = static_cast<uint8_t *>(at(v.hidden_s));
           else fp.hidden_scales = static_cast<float *>(at(v.hidden_s));
         }
-        launch_front(fp, s);
+        if (by_expert && local_front_fits(call->tokens, call->experts, call->hidden_size, call->top))
+          launch_local_front(fp, s);
+        else
+          launch_front(fp, s);
         if (int32_t status = launched(call, "router, topk and sort")) return status;
       }
     } else if (prefill_front) {

@@ -118,8 +118,9 @@ __device__ __forceinline__ void argmax_step(float &best, int &expert) {
 /// Routes one token with `kIter` scores per lane (the expert count in whole halves, rounded up to
 /// a power of two: the extra slots hold -inf and add exact zeros to the sum). kDevice: the scores
 /// are read and the ids stored at device scope (scores and ids cross workgroups of one launch).
+/// Answers, in lane k < top of an active token, the id it stored (-1 in the other lanes).
 template <int kIter, bool kDevice>
-__device__ __forceinline__ void route(const void *scores, int score_kind, int64_t row_stride,
+__device__ __forceinline__ int32_t route(const void *scores, int score_kind, int64_t row_stride,
                                       int row, int experts, int top, int renormalize,
                                       const void *scale, int scale_kind, int32_t *ids,
                                       float *weights, const int32_t *map, const int32_t *live,
@@ -211,7 +212,7 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
     const float total = partial < FLT_EPSILON ? FLT_EPSILON : partial;
     weight = weight / total;
   }
-  if (!active || lane >= top) return;
+  if (!active || lane >= top) return -1;
   const bool named = picked_expert >= 0 && picked_expert < experts;
   if (scale_kind != -1 && scale != nullptr && named) weight = weight * load_kind(scale, scale_kind, picked_expert);
   const int64_t slot = static_cast<int64_t>(row) * top + lane;
@@ -220,6 +221,7 @@ __device__ __forceinline__ void route(const void *scores, int score_kind, int64_
   else ids[slot] = id;
   weights[slot] = weight;
   if (load != nullptr && named && (live == nullptr || row < live[0])) atomicAdd(load + picked_expert, 1ull);
+  return id;
 }
 
 
