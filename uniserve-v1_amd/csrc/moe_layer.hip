@@ -118,7 +118,32 @@ namespace {
 /// moe_sort over the window's experts, as the layer calls it.
 int32_t run_sort(const uniserve_moe_layer_call *call, int32_t *ids, float *weights, int32_t *t2e, int32_t *t2l,
                  int32_t *e2p, int32_t *p2e, int32_t *p2t, int32_t *padded, int32_t *tiles, int64_t local_experts,
-                 void *stream) {
+                 int32_t *scratch, void *stream) {
+  const int64_t routes = call->tokens * call->top;
+  if (scratch != nullptr && uniserve::layer_sort_two_launches(routes, local_experts)) {
+    // Above one workgroup's routes: the count, then the scan folded into the placement, with the
+    // per-chunk counts in `scratch`.
+    uniserve::sort::SortParams p{};
+    p.ids = ids;
+    p.tile_to_expert = t2e;
+    p.tile_to_limit = t2l;
+    p.expanded_to_permuted = e2p;
+    p.permuted_to_expanded = p2e;
+    p.permuted_to_token = p2t;
+    p.total_padded_tokens = padded;
+    p.num_non_exiting_tiles = tiles;
+    p.live_tokens = call->live_tokens;
+    p.routes = routes;
+    p.top = call->top;
+    p.local_experts = static_cast<int32_t>(local_experts);
+    p.local_offset = static_cast<int32_t>(call->local_offset);
+    p.tile = static_cast<int32_t>(kTile);
+    int bits = 0;
+    while ((1ll << bits) <= local_experts) ++bits;
+    p.key_bits = bits;
+    uniserve::launch_layer_sort(p, scratch, static_cast<hipStream_t>(stream));
+    return uniserve::launched(call, "moe_sort");
+  }
   uniserve_moe_sort_call sort{};
   sort.ids = ids;
   sort.scales = weights;
@@ -333,6 +358,14 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     int32_t *p2t = static_cast<int32_t *>(at(v.permuted_to_token));
     int32_t *padded = static_cast<int32_t *>(at(v.total_padded_tokens));
     int32_t *tiles = static_cast<int32_t *>(at(v.num_non_exiting_tiles));
+    // The sort's per-chunk counts: the last bytes of the products' rows, which only FC2 writes,
+    // later (the MXFP4 prefill front end parks its token-major scales at their start).
+    const int64_t products_bytes = v.permuted_rows * call->hidden_size * 2;
+    const int64_t sort_bytes = (layer_sort_scratch_bytes(call->tokens * call->top, local_experts) + 255) / 256 * 256;
+    int32_t *sort_scratch =
+        sort_bytes + call->tokens * (call->hidden_size / 32) <= products_bytes
+            ? reinterpret_cast<int32_t *>(static_cast<char *>(at(v.products)) + products_bytes - sort_bytes)
+            : nullptr;
 
     // Decode sizes: router, topk and sort in one launch (at the ROUTER step; TOPK and SORT launch
     // nothing).
@@ -414,7 +447,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         if (int32_t status = launched(call, "router and topk")) return status;
       }
       if (want(UNISERVE_MOE_LAYER_SORT)) {
-        if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, stream))
+        if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, sort_scratch, stream))
           return status;
       }
     } else {
@@ -439,7 +472,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
 
     // 3. moe_sort over the window's experts.
     if (want(UNISERVE_MOE_LAYER_SORT)) {
-      if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, stream))
+      if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, sort_scratch, stream))
         return status;
     }
     }

@@ -217,7 +217,9 @@ __device__ __forceinline__ void split_count(const SortParams &p, int64_t first, 
   }
 }
 
-__global__ void __launch_bounds__(kSplitThreads) sort_count_kernel(SortParams p) {
+/// `counts` null: each chunk's counts are parked at the head of its stretch of
+/// expanded_to_permuted (the entry's three-launch path); else they go to counts[chunk][E].
+__global__ void __launch_bounds__(kSplitThreads) sort_count_kernel(SortParams p, int32_t *counts) {
   extern __shared__ int32_t lds[];
   const int E = p.local_experts;
   int32_t *wave_rows = lds;  // [kSplitWaves][E]
@@ -231,7 +233,8 @@ __global__ void __launch_bounds__(kSplitThreads) sort_count_kernel(SortParams p)
   for (int e = threadIdx.x; e < E; e += kSplitThreads) {
     int32_t sum = 0;
     for (int w = 0; w < kSplitWaves; ++w) sum += wave_rows[w * E + e];
-    p.expanded_to_permuted[first + e] = sum;
+    if (counts != nullptr) counts[static_cast<int64_t>(blockIdx.x) * E + e] = sum;
+    else p.expanded_to_permuted[first + e] = sum;
   }
 }
 
@@ -360,7 +363,138 @@ __global__ void __launch_bounds__(kSplitThreads) sort_place_kernel(SortParams p)
   }
 }
 
+/// The scan folded into the placement (the layer's path: the counts sit in a scratch table that no
+/// placement overwrites, so every workgroup reads all of them): each workgroup sums every chunk's
+/// counts per expert (the totals) and those of the chunks before its own (its base in each
+/// expert), scans the experts' tiles, and places its chunk; workgroup 0 also writes the tile
+/// tables, the padding rows and the two counts. Every map entry as the three-launch path writes it.
+__global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortParams p, const int32_t *counts) {
+  extern __shared__ int32_t lds[];
+  const int E = p.local_experts;
+  int32_t *start = lds;              // [E] this chunk's first row in each expert
+  int32_t *wave_rows = start + E;    // [kSplitWaves][E]
+  int32_t *total = wave_rows + kSplitWaves * E;   // [E]
+  int32_t *first_row = total + E;                 // [E]
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
+  const int64_t chunks = p.routes / kSplitChunk;
+  const int64_t own = blockIdx.x;
+  constexpr int kBatchChunks = 16;
+
+  for (int e = threadIdx.x; e < E; e += kSplitThreads) {
+    int32_t running = 0, before = 0;
+    for (int64_t c0 = 0; c0 < chunks; c0 += kBatchChunks) {
+      int32_t count[kBatchChunks];
+#pragma unroll
+      for (int u = 0; u < kBatchChunks; ++u) count[u] = c0 + u < chunks ? counts[(c0 + u) * E + e] : 0;
+#pragma unroll
+      for (int u = 0; u < kBatchChunks; ++u) {
+        if (c0 + u == own) before = running;
+        running += count[u];
+      }
+    }
+    total[e] = running;
+    start[e] = before;
+  }
+  for (int i = threadIdx.x; i < kSplitWaves * E; i += kSplitThreads) wave_rows[i] = 0;
+  __syncthreads();
+
+  if (wave == 0) {
+    int32_t carried = 0;
+    for (int base = 0; base < E; base += kWave) {
+      const int e = base + lane;
+      const int32_t tiles = e < E ? (total[e] + p.tile - 1) / p.tile : 0;
+      int32_t inclusive = tiles;
+#pragma unroll
+      for (int offset = 1; offset < kWave; offset *= 2) {
+        const int32_t other = __shfl_up(inclusive, offset);
+        if (lane >= offset) inclusive += other;
+      }
+      if (e < E) first_row[e] = (carried + inclusive - tiles) * p.tile;
+      carried += __shfl(inclusive, kWave - 1);
+    }
+    if (blockIdx.x == 0 && lane == 0) {
+      p.total_padded_tokens[0] = carried * p.tile;
+      p.num_non_exiting_tiles[0] = carried;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kSplitThreads) start[e] += first_row[e];
+
+  if (blockIdx.x == 0) {
+    // Tile tables and the padding rows of each expert's last tile, one wavefront per expert.
+    for (int e = wave; e < E; e += kSplitWaves) {
+      const int32_t count = total[e];
+      if (count == 0) continue;
+      const int32_t first = first_row[e];
+      const int32_t tiles = (count + p.tile - 1) / p.tile;
+      const int32_t first_tile = first / p.tile;
+      for (int32_t t = lane; t < tiles; t += kWave) {
+        const int32_t end_of_tile = (first_tile + t + 1) * p.tile;
+        const int32_t end_of_rows = first + count;
+        p.tile_to_expert[first_tile + t] = e;
+        p.tile_to_limit[first_tile + t] = end_of_tile < end_of_rows ? end_of_tile : end_of_rows;
+      }
+      for (int32_t row = count + lane; row < tiles * p.tile; row += kWave) {
+        p.permuted_to_expanded[first + row] = -1;
+        p.permuted_to_token[first + row] = -1;
+      }
+    }
+  }
+
+  int64_t first, past, slice_first, slice_past;
+  split_chunk(p, &first, &past);
+  split_count(p, first, past, live, wave_rows, &slice_first, &slice_past);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kSplitThreads) {
+    int32_t running = start[e];
+    for (int w = 0; w < kSplitWaves; ++w) {
+      const int32_t count = wave_rows[w * E + e];
+      wave_rows[w * E + e] = running;
+      running += count;
+    }
+  }
+  __syncthreads();
+  int32_t *mine = wave_rows + wave * E;
+  for (int64_t base = slice_first; base < slice_past; base += kWave) {
+    const int64_t route = base + lane;
+    const bool inside = route < slice_past;
+    const int32_t e = inside ? local_expert(p, route, live) : -1;
+    const uint64_t peers = match_any(static_cast<uint32_t>(e + 1), p.key_bits);
+    if (e >= 0) {
+      const int32_t row = mine[e] + __popcll(peers & below);
+      p.expanded_to_permuted[route] = row;
+      p.permuted_to_expanded[row] = static_cast<int32_t>(route);
+      p.permuted_to_token[row] = static_cast<int32_t>(route / p.top);
+    } else if (inside) {
+      p.expanded_to_permuted[route] = route < live ? -1 : -2;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0 && (peers & below) == 0) mine[e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 }  // namespace
+
+bool layer_sort_two_launches(int64_t routes, int64_t local_experts) {
+  return routes > sort::kChunk && 2 * local_experts <= kSplitChunk;
+}
+
+int64_t layer_sort_scratch_bytes(int64_t routes, int64_t local_experts) {
+  return routes / kSplitChunk * local_experts * static_cast<int64_t>(sizeof(int32_t));
+}
+
+void launch_layer_sort(const sort::SortParams &p, int32_t *counts, hipStream_t stream) {
+  const uint32_t chunks = static_cast<uint32_t>(p.routes / kSplitChunk);
+  const size_t count_bytes = kSplitWaves * p.local_experts * sizeof(int32_t);
+  hipLaunchKernelGGL(sort_count_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes, stream, p, counts);
+  hipLaunchKernelGGL(sort_scan_place_kernel, dim3(chunks), dim3(kSplitThreads),
+                     count_bytes + 3 * p.local_experts * sizeof(int32_t), stream, p, static_cast<const int32_t *>(counts));
+}
+
 }  // namespace uniserve
 
 extern "C" int32_t uniserve_moe_sort(const uniserve_moe_sort_call *call, void *stream) {
@@ -419,7 +553,7 @@ extern "C" int32_t uniserve_moe_sort(const uniserve_moe_sort_call *call, void *s
     }
     const uint32_t chunks = static_cast<uint32_t>(p.routes / kSplitChunk);
     const size_t count_bytes = kSplitWaves * call->local_experts * sizeof(int32_t);
-    hipLaunchKernelGGL(sort_count_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes, s, p);
+    hipLaunchKernelGGL(sort_count_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes, s, p, nullptr);
     hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kSortThreads), 2 * call->local_experts * sizeof(int32_t), s, p);
     hipLaunchKernelGGL(sort_place_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes + call->local_experts * sizeof(int32_t),
                        s, p);
