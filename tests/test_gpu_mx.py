@@ -243,3 +243,42 @@ def test_device_mxfp4_quantiser_matches_the_oracle(device):
     want_pairs, want_scales = O.quantize_blocks_mxfp4(bf16_bits(w))
     np.testing.assert_array_equal(scales.cpu().numpy(), want_scales)
     np.testing.assert_array_equal(pairs.cpu().numpy(), want_pairs)
+
+
+def test_prefill_fc1_quantises_like_the_mxfp8_quantiser(device):
+    """At prefill shapes the layer's MX FC1 writes the gated rows straight in FC2's MXFP8 form: codes
+    and stage-major E8M0 bytes of every live row equal the stand-alone FC1 (bf16 out) followed by
+    the stand-alone MXFP8 quantiser."""
+    tokens, hidden, experts, top, intermediate = 4096, 2048, 128, 8, 768
+    announce("fused mx FC1 quantisation")
+    x, router, host_w = mx_layer_inputs(device, tokens, hidden, experts, intermediate, 33)
+    w1, s1, w2, s2 = on(device, host_w)
+    s1, s2 = ops.mx_stage_major_scales(s1), ops.mx_stage_major_scales(s2)
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f4e2m1")
+    layer(x, router, w1, w2, up_gate_scales=s1, down_scales=s2, scale_layout="stage")
+    torch.cuda.synchronize()
+    assert layer.views.route_scales == 1
+    rows = layer.views.permuted_rows
+
+    class Maps:
+        def __getitem__(self, index):
+            name = ["tile_to_expert", "tile_to_limit", "expanded_to_permuted", "permuted_to_expanded",
+                    "permuted_to_token", "total_padded_tokens", "num_non_exiting_tiles"][index]
+            length = {0: layer.views.max_tiles, 1: layer.views.max_tiles, 2: tokens * top, 3: rows, 4: rows,
+                      5: 1, 6: 1}[index]
+            return layer.view(name, torch.int32, (length,))
+
+    xq, xs = ops.quantize_mxfp8(x)
+    gated = ops.gather_gemm_mx(xq, xs, w1, s1, top, Maps(), rows, scale_layout="stage")
+    want_q, want_s = ops.quantize_mxfp8(gated)
+    torch.cuda.synchronize()
+    p2e = layer.view("permuted_to_expanded", torch.int32, (rows,)).cpu().numpy()
+    padded = int(layer.view("total_padded_tokens", torch.int32, (1,)).cpu().numpy()[0])
+    live = np.nonzero(p2e[:padded] >= 0)[0]
+    assert live.size == tokens * top
+    got_q = layer.view("gated_q", torch.uint8, (rows, intermediate)).cpu().numpy()
+    np.testing.assert_array_equal(got_q[live], want_q.cpu().numpy()[live])
+    # Stage-major bytes: [intermediate / 128 stages][rows][4 blocks] -> [rows][intermediate / 32].
+    table = layer.view("gated_s", torch.uint8, (intermediate // 128, rows, 4)).cpu().numpy()
+    got_s = np.ascontiguousarray(table.transpose(1, 0, 2)).reshape(rows, intermediate // 32)
+    np.testing.assert_array_equal(got_s[live], want_s.cpu().numpy()[live])

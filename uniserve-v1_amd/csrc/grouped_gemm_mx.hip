@@ -132,6 +132,12 @@ struct MxParams {
   int64_t local_offset;
   int64_t local_experts;
   int32_t compact;
+  // FC1 on the tiled kernel only, or null: the gated rows are written as MXFP8 codes
+  // [permuted_rows, out_width] with their E8M0 bytes stage-major by permuted row
+  // ([out_width / 128, code_scale_rows, 4]) instead of bf16 rows - FC2's operand.
+  uint8_t *out_codes;
+  uint8_t *out_code_scales;
+  int64_t code_scale_rows;
 };
 
 /// Stride words of a scale table with `rows` rows in `layout`.
@@ -623,6 +629,28 @@ __global__ void __launch_bounds__(kWaves * kWave, 8 / kWaves) tiled_mx_kernel(Mx
     }
   }
   __syncthreads();
+  if (kGated && p.out_codes != nullptr) {
+    // The gated rows as FC2's MXFP8 operand, straight from the staged bf16 tile (the quantiser's
+    // rounding points and encoding: each 32-column block by four lanes, its E8M0 byte from the
+    // block's bf16 values): the slice's 128 columns are one 128-element stage, so each row's four
+    // scale bytes make its one stage-major word. Live rows only.
+    constexpr int kLanesPerRow = kOutCols / 8;  // 16
+    const int sub = t % kLanesPerRow;
+    uint8_t *stage_scales = p.out_code_scales + (slice_col / 128) * p.code_scale_rows * 4;
+    for (int m = t / kLanesPerRow; m < kTileRows; m += kThreadsHere / kLanesPerRow) {
+      if (m >= rows) continue;  // a row's lanes are the four lanes of each of its blocks
+      const u32x4 packed = *reinterpret_cast<const u32x4 *>(tile_lds + m * kOutStride + sub * 16);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(packed[j] << 16);
+        v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
+      }
+      const uint32_t scale = mxfp8_eight(v, p.out_codes + (first + m) * p.out_width + slice_col + sub * 8);
+      if ((sub & 3) == 0) stage_scales[(first + m) * 4 + sub / 4] = static_cast<uint8_t>(scale);
+    }
+    return;
+  }
   constexpr int kPieces = kOutCols / 8;
   for (int index = t; index < kTileRows * kPieces; index += kThreadsHere) {
     const int m = index / kPieces;
@@ -719,7 +747,8 @@ bool mx_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidde
          !fp8_stream_path(routes_bound, experts) && tiled_fits(false, intermediate, hidden_size);
 }
 
-int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, int32_t activation, void *stream) {
+int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, int32_t activation, void *stream,
+                       uint8_t *out_codes, uint8_t *out_code_scales) {
   return guarded(call, [&]() -> int32_t {
     if (call->out_dtype != UNISERVE_DTYPE_BF16) return UNISERVE_REFUSE(call, "gather_gemm_mx writes bf16 only");
     if (call->hidden == nullptr || call->hidden_scales == nullptr || call->weights == nullptr ||
@@ -765,10 +794,18 @@ int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, 
     scale_strides(scale_rows != 0 ? UNISERVE_MX_SCALES_STAGE_MAJOR : UNISERVE_MX_SCALES_ROW_MAJOR, scale_rows, p.K,
                   &p.as_stage, &p.as_row);
     p.as_by_route = scale_rows != 0 ? 1 : 0;
-    if (!fp8_stream_path(call->tokens * call->top, call->experts) && tiled_fits(true, p.K, p.out_width))
+    if (!fp8_stream_path(call->tokens * call->top, call->experts) && tiled_fits(true, p.K, p.out_width)) {
+      if (out_codes != nullptr) {
+        if (scale_rows == 0) return UNISERVE_REFUSE(call, "gather_gemm_mx: quantised rows need route-major scales");
+        p.out_codes = out_codes;
+        p.out_code_scales = out_code_scales;
+        p.code_scale_rows = scale_rows;
+      }
       launch_tiled_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
-    else
+    } else {
+      if (out_codes != nullptr) return UNISERVE_REFUSE(call, "gather_gemm_mx: quantised rows only on the tiled kernel");
       launch_mx(p, true, max_tiles, static_cast<hipStream_t>(stream));
+    }
     return launched(call, "gather_gemm_mx");
   });
 }

@@ -60,7 +60,11 @@ bool mx_route_scales(int64_t tokens, int64_t top, int64_t experts, int64_t hidde
 
 /// The product entries; with `scale_rows` nonzero the activation scales are stage-major by
 /// permuted row ([K / 128, scale_rows, 4], scale_rows >= permuted_rows).
-int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, int32_t activation, void *stream);
+/// `out_codes` (with `out_code_scales`; route-major scales, the tiled kernel only): FC1 writes the
+/// gated rows as MXFP8 codes and stage-major E8M0 bytes by permuted row, bit for bit what
+/// uniserve_quantize_mxfp8 makes of the bf16 rows, and no bf16 rows.
+int32_t gather_gemm_mx(const uniserve_gather_mx_call *call, int64_t scale_rows, int32_t activation, void *stream,
+                       uint8_t *out_codes = nullptr, uint8_t *out_code_scales = nullptr);
 int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, void *stream);
 
 }  // namespace uniserve

@@ -231,7 +231,10 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   } else if (by_expert != nullptr) {
     gather_gemm_mx_by_expert(&fc1, *by_expert, static_cast<int32_t>(call->activation), stream);
     if (int32_t status = launched(call, "gather_gemm_mx")) return status;
-  } else if (gather_gemm_mx(&fc1, scale_rows, static_cast<int32_t>(call->activation), stream) != 0) {
+  } else if (gather_gemm_mx(&fc1, scale_rows, static_cast<int32_t>(call->activation), stream,
+                            scale_rows != 0 ? static_cast<uint8_t *>(at(v.gated_q)) : nullptr,
+                            scale_rows != 0 ? static_cast<uint8_t *>(at(v.gated_s)) : nullptr) != 0) {
+    // (Prefill shapes, route-major scales: FC1 writes its rows already as FC2's MXFP8 operand.)
     return forward_error(call, "gather_gemm_mx", fc1);
   }
 
@@ -244,12 +247,8 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   qg.rows = by_expert != nullptr ? by_expert->routes : v.permuted_rows;
   qg.width = call->intermediate;
   qg.input_dtype = UNISERVE_DTYPE_BF16;
-  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_GATED)) {
-  } else if (scale_rows != 0) {
-    launch_quantize_mxfp8(at(v.gated), false, static_cast<uint8_t *>(at(v.gated_q)), nullptr, qg.row_limit,
-                          v.permuted_rows, call->intermediate, s, static_cast<uint8_t *>(at(v.gated_s)), nullptr, 0,
-                          scale_rows);
-    if (int32_t status = launched(call, "quantize_mxfp8")) return status;
+  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) || scale_rows != 0) {
+    // (With route-major scales FC1 wrote the quantised rows itself.)
   } else if (uniserve_quantize_mxfp8(&qg, stream) != 0) {
     return forward_error(call, "quantize_mxfp8", qg);
   }
