@@ -125,12 +125,18 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer(const struct uniserve_moe_layer_cal
 /// serialise them.
 UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_layer_call *call, void *stream);
 
-/// The layer's launches in order; the quantiser steps launch nothing for bf16 weights,
-/// QUANTIZE_GATED launches nothing where the e4m3 FC1 writes its rows already quantised, and
-/// QUANTIZE_HIDDEN nothing for e4m3 and MXFP4 at decode sizes (the ROUTER launch quantises). At
-/// decode sizes (at most 4096 routes over at most 512 local experts, a router of at most 1024
-/// experts) ROUTER launches the router, topk and sort as one kernel (no sort where the layer
-/// skips it), and TOPK and SORT launch nothing.
+/// The layer's launches in order. Which step launches what depends on the call's size:
+/// - decode sizes (at most 4096 routes over at most 512 local experts, a router of at most 1024
+///   experts): ROUTER launches the front end - router scores and topk, plus the sort where the
+///   layer does not skip it, plus the hidden rows' e4m3 / MXFP8 quantisation for those weights -
+///   and TOPK, SORT and QUANTIZE_HIDDEN launch nothing;
+/// - prefill sizes (at most 128 experts, hidden a multiple of 128): ROUTER launches router scores,
+///   topk and the hidden rows' quantisation in one kernel, TOPK launches nothing, SORT the sort,
+///   and QUANTIZE_HIDDEN only the copy of each token's scales to its routes' rows where the
+///   products take them route-major (views.route_scales);
+/// - otherwise each step launches its own operator.
+/// The quantiser steps launch nothing for bf16 weights, and QUANTIZE_GATED nothing where FC1
+/// writes its rows already quantised (e4m3 in the layer; MXFP4 with route-major scales).
 enum uniserve_moe_layer_step {
   UNISERVE_MOE_LAYER_ROUTER = 0,
   UNISERVE_MOE_LAYER_TOPK = 1,

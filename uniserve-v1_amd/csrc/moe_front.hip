@@ -25,6 +25,7 @@
 #include "moe_front.hpp"
 #include "sort_small.hpp"
 #include "topk_route.hpp"
+#include "front_token.hpp"
 
 namespace uniserve {
 namespace {
@@ -212,158 +213,33 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontParams p) {
 // ---- the front end without a sort: one workgroup per token ------------------------------------------
 //
 // Where the layer skips the sort (the expert-major products find their routes themselves), nothing
-// crosses workgroups: each workgroup takes one token, streams the whole router matrix (16
-// wavefronts: wavefront w the experts w, w + 16, ..., one or two rows per pass with the next pass's
-// loads in flight, each row as whole 1 KB lines: lane l holds channels 512 c + 8 l .. + 7),
-// reduces each expert's per-lane FP32 partial sums across the wavefront, adds the bias and rounds
-// once into bf16, and routes the token
-// from its scores in LDS (the topk routine, one 32-lane half); the id's lane writes the route's
-// expanded_to_permuted entry. No tickets, no device-scope hand-offs. e4m3 and MXFP4 layers: the
-// first wavefront quantises the token's hidden row from the copy it holds in registers (the
-// quantisers' group routines: codes and scales bit for bit theirs).
+// crosses workgroups: each 16-wavefront workgroup takes one token through front_token::route_one
+// (front_token.hpp). No tickets, no device-scope hand-offs.
 
-constexpr int kLocalChunk = 512;          // channels of one row per wavefront load (64 lanes x 8)
-constexpr int kLocalMaxExperts = 128;     // four scores per lane of the routing half
-constexpr int64_t kLocalMinTokens = 32;
-
-__device__ __forceinline__ float dot8_bf16(const u32x4 &a, const u32x4 &b, float sum) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sum = __builtin_fmaf(__uint_as_float(a[j] << 16), __uint_as_float(b[j] << 16), sum);
-    sum = __builtin_fmaf(__uint_as_float(a[j] & 0xffff0000u), __uint_as_float(b[j] & 0xffff0000u), sum);
-  }
-  return sum;
-}
-
-/// kChunks: at most that many 512-channel chunks per row (4: hidden <= 2048, two router rows in
-/// flight per wavefront; 8: hidden <= 4096, one); kQuant: 0 none, 1 e4m3, 2 MXFP8.
+/// kChunks: at most that many 512-channel chunks per row (4: hidden <= 2048; 8: hidden <= 4096);
+/// kQuant: 0 none, 1 e4m3, 2 MXFP8.
 template <int kChunks, int kQuant>
 __global__ void __launch_bounds__(kThreads) local_front_kernel(FrontParams p) {
-  constexpr int kRows = 8 / kChunks;  // router rows a wavefront loads together
-  __shared__ uint16_t scores[kLocalMaxExperts];
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-  const int lane = lane_id();
-  const int64_t token = blockIdx.x;
-  const int chunks = static_cast<int>(p.hidden / kLocalChunk);
-  const int experts = static_cast<int>(p.experts);
-
-  u32x4 xs[kChunks];
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c)
-    xs[c] = c < chunks ? *reinterpret_cast<const u32x4 *>(p.x + token * p.hidden + c * kLocalChunk + 8 * lane)
-                       : u32x4{0, 0, 0, 0};
-
-  // Wavefront w: experts w, w + 16, ..., kRows of them per pass; the next pass's rows are loaded
-  // while this pass's are multiplied, and every lane keeps its partial sum of each of its experts,
-  // reduced across the wavefront at the end (the experts' reductions interleaved).
-  constexpr int kPerWave = kLocalMaxExperts / kWaves;  // 8
-  constexpr int kPasses = kPerWave / kRows;
-  u32x4 w[2][kRows][kChunks];
-  float partial[kPerWave];
-  auto load_pass = [&](int pass, int buffer) {
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      const int slot = pass * kRows + r;
-      const int e = wave + slot * kWaves < experts ? wave + slot * kWaves : wave;
-      const uint16_t *row = p.w + static_cast<int64_t>(e < experts ? e : 0) * p.hidden + 8 * lane;
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-        if (c < chunks) w[buffer][r][c] = *reinterpret_cast<const u32x4 *>(row + c * kLocalChunk);
-    }
-  };
-  load_pass(0, 0);
-#pragma unroll
-  for (int pass = 0; pass < kPasses; ++pass) {
-    if (pass + 1 < kPasses) load_pass(pass + 1, (pass + 1) & 1);
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      float sum = 0.0f;
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-        if (c < chunks) sum = dot8_bf16(w[pass & 1][r][c], xs[c], sum);
-      partial[pass * kRows + r] = sum;
-    }
-  }
-#pragma unroll
-  for (int offset = 32; offset >= 1; offset /= 2)
-#pragma unroll
-    for (int i = 0; i < kPerWave; ++i) partial[i] += __shfl_xor(partial[i], offset);
-  if (lane < kPerWave) {
-    float sum = partial[0];
-#pragma unroll
-    for (int i = 1; i < kPerWave; ++i) sum = lane == i ? partial[i] : sum;
-    const int e = wave + lane * kWaves;
-    if (e < experts) {
-      if (p.bias != nullptr) sum += p.bias[e];
-      const uint16_t bits = f32_to_bf16(sum);
-      scores[e] = bits;
-      p.scores[token * experts + e] = bits;
-    }
-  }
-
-  // The hidden row's quantisation, first wavefront: lane l's slice of chunk c is channels
-  // 512 c + 8 l .. + 7, in 128-channel group 4 c + l / 16 (16 lanes each) or 32-channel block
-  // (512 c + 8 l) / 32 (4 lanes each).
-  if constexpr (kQuant != 0) {
-    if (wave == 0) {
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c) {
-        if (c >= chunks) break;
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[2 * j] = __uint_as_float(xs[c][j] << 16);
-          v[2 * j + 1] = __uint_as_float(xs[c][j] & 0xffff0000u);
-        }
-        uint8_t *codes = p.hidden_codes + token * p.hidden + c * kLocalChunk + 8 * lane;
-        if constexpr (kQuant == 2) {
-          const uint32_t scale = mxfp8_eight(v, codes);
-          if ((lane & 3) == 0)
-            p.hidden_mx_scales[token * (p.hidden / 32) + (c * kLocalChunk + 8 * lane) / 32] = static_cast<uint8_t>(scale);
-        } else {
-          float amax = 0.0f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
-          amax = row16_max(amax);
-          const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-          *reinterpret_cast<uint2 *>(codes) = e4m3_eight_of_bf16(v, scale);
-          if ((lane & 15) == 0) p.hidden_scales[token * (p.hidden / 128) + 4 * c + lane / 16] = scale;
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // Routing by the first 32-lane half; each pick's lane writes its route's entry.
-  if (threadIdx.x < topk::kHalf) {
-    const int32_t id = topk::route<kLocalMaxExperts / topk::kHalf, false>(
-        scores, 1, experts, static_cast<int>(token), experts, p.top, p.renormalize, nullptr, -1, p.ids, p.weights,
-        p.map, p.live, p.load, true, 0);
-    const int k = static_cast<int>(threadIdx.x);
-    if (k < p.top) {
-      const int64_t route = token * p.top + k;
-      const int64_t live = (p.live != nullptr ? static_cast<int64_t>(p.live[0]) : p.tokens) * p.top;
-      const int64_t local = static_cast<int64_t>(id) - p.sort.local_offset;
-      const bool visible = route < live && local >= 0 && local < p.sort.local_experts;
-      p.sort.expanded_to_permuted[route] = visible ? static_cast<int32_t>(route) : -1;
-    }
-  }
+  __shared__ uint16_t scores[front_token::kMaxExperts];
+  front_token::route_one<kWaves, kChunks, kQuant>(p, blockIdx.x, scores);
 }
 
 }  // namespace
 
+constexpr int64_t kLocalMinTokens = 32;
+
 bool local_front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top) {
   // Each workgroup streams the whole router matrix: for a few tokens the tile-split front end,
   // whose workgroups read a share each, is the faster (235B, one token: 16 us against 18).
-  return tokens >= kLocalMinTokens && tokens <= 0x7fffffffLL && experts >= 1 && experts <= kLocalMaxExperts &&
-         hidden % kLocalChunk == 0 && hidden / kLocalChunk <= 8 && top >= 1 && top <= topk::kHalf &&
-         top <= experts;
+  return tokens >= kLocalMinTokens && tokens <= 0x7fffffffLL && experts >= 1 &&
+         experts <= front_token::kMaxExperts && hidden % front_token::kChunk == 0 &&
+         hidden / front_token::kChunk <= 8 && top >= 1 && top <= topk::kHalf && top <= experts;
 }
 
 void launch_local_front(const FrontParams &p, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(p.tokens));
   const int quant = p.hidden_codes == nullptr ? 0 : (p.hidden_mx_scales != nullptr ? 2 : 1);
-  const bool narrow = p.hidden <= 4 * kLocalChunk;
+  const bool narrow = p.hidden <= 4 * front_token::kChunk;
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, p); };
   if (narrow && quant == 0) go(local_front_kernel<4, 0>);
   else if (narrow && quant == 1) go(local_front_kernel<4, 1>);
