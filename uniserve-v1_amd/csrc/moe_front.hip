@@ -224,7 +224,117 @@ __global__ void __launch_bounds__(kThreads) local_front_kernel(FrontParams p) {
   front_token::route_one<kWaves, kChunks, kQuant>(p, blockIdx.x, scores);
 }
 
+// ---- the front end for a few tokens without a sort: experts split over workgroups -------------------
+//
+// A one-token step is latency-bound: the tile-split kernel above gives the router's 16-expert
+// tiles to eight workgroups (128 KB each at 4096 channels) and a workgroup per token would stream
+// the whole matrix alone. Here each wavefront owns one expert (its row in registers, whole 1 KB
+// lines: lane l holds channels 512 c + 8 l .. + 7 of chunk c, as in front_token.hpp) and takes the
+// tokens one after another: the dot product in FP32, an xor-butterfly reduction, the bias, one
+// rounding into bf16, a device-scope store. Each workgroup then quantises its share of the hidden
+// rows (e4m3 / MXFP8), and the last workgroup to take the ticket routes every token, one per
+// 32-lane half, writing the ids, weights and each route's expanded_to_permuted entry from the id
+// the routine answers.
+
+constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / kWave;  // experts per workgroup
+constexpr int64_t kSplitMaxTokens = kSplitThreads / topk::kHalf;
+
+template <int kChunks, int kQuant>
+__global__ void __launch_bounds__(kSplitThreads) split_front_kernel(FrontParams p) {
+  __shared__ int32_t flag;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int lane = lane_id();
+  const int chunks = static_cast<int>(p.hidden / front_token::kChunk);
+  const int64_t expert = static_cast<int64_t>(blockIdx.x) * kSplitWaves + wave;
+  const bool named = expert < p.experts;
+
+  u32x4 w[kChunks];
+  const uint16_t *row = p.w + (named ? expert : 0) * p.hidden + 8 * lane;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c)
+    if (c < chunks) w[c] = *reinterpret_cast<const u32x4 *>(row + c * front_token::kChunk);
+  const float bias = named && p.bias != nullptr ? p.bias[expert] : 0.0f;
+  for (int64_t t = 0; t < p.tokens; ++t) {
+    const uint16_t *x = p.x + t * p.hidden + 8 * lane;
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+      if (c < chunks) sum = front_token::dot8_bf16(w[c], *reinterpret_cast<const u32x4 *>(x + c * front_token::kChunk), sum);
+#pragma unroll
+    for (int offset = 32; offset >= 1; offset /= 2) sum += __shfl_xor(sum, offset);
+    if (lane == 0 && named) {
+      if (p.bias != nullptr) sum += bias;
+      store_device(p.scores + t * p.experts + expert, f32_to_bf16(sum));
+    }
+  }
+
+  // This workgroup's share of the hidden rows' quantisation (the quantisers' routines).
+  if constexpr (kQuant == 1) {
+    const int64_t per_row = p.hidden / 128;
+    const int64_t groups = p.tokens * per_row;
+    const int64_t stride = static_cast<int64_t>(kSplitThreads / 16) * gridDim.x;
+    for (int64_t g = blockIdx.x + static_cast<int64_t>(threadIdx.x / 16) * gridDim.x; g < groups; g += stride) {
+      const int64_t t = g / per_row, column = (g % per_row) * 128;
+      quantize_bf16_group(p.x + t * p.hidden + column, p.hidden_codes + t * p.hidden + column,
+                          p.hidden_scales + t * per_row + g % per_row, static_cast<int>(threadIdx.x & 15));
+    }
+  } else if constexpr (kQuant == 2) {
+    const int64_t per_row = p.hidden / 32;
+    const int64_t blocks = p.tokens * per_row;
+    const int64_t stride = static_cast<int64_t>(kSplitThreads / 4) * gridDim.x;
+    const int sub = static_cast<int>(threadIdx.x & 3);
+    for (int64_t b = blockIdx.x + static_cast<int64_t>(threadIdx.x / 4) * gridDim.x; b < blocks; b += stride) {
+      const int64_t t = b / per_row, column = (b % per_row) * 32 + sub * 8;
+      const u32x4 packed = *reinterpret_cast<const u32x4 *>(p.x + t * p.hidden + column);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(packed[j] << 16);
+        v[2 * j + 1] = __uint_as_float(packed[j] & 0xffff0000u);
+      }
+      const uint32_t scale = mxfp8_eight(v, p.hidden_codes + t * p.hidden + column);
+      if (sub == 0) p.hidden_mx_scales[t * per_row + b % per_row] = static_cast<uint8_t>(scale);
+    }
+  }
+
+  // The last workgroup routes every token, one per 32-lane half.
+  if (!last_ticket(p.ticket + 1, gridDim.x, &flag)) return;
+  const int half = static_cast<int>(threadIdx.x) / topk::kHalf;
+  if (half >= p.tokens) return;
+  const int32_t id = topk::route<front_token::kMaxExperts / topk::kHalf, true>(
+      p.scores, 1, p.experts, half, static_cast<int>(p.experts), p.top, p.renormalize, nullptr, -1, p.ids,
+      p.weights, p.map, p.live, p.load, true, half);
+  const int k = static_cast<int>(threadIdx.x) & (topk::kHalf - 1);
+  if (k < p.top) {
+    const int64_t route = static_cast<int64_t>(half) * p.top + k;
+    const int64_t live = (p.live != nullptr ? static_cast<int64_t>(p.live[0]) : p.tokens) * p.top;
+    const int64_t local = static_cast<int64_t>(id) - p.sort.local_offset;
+    const bool visible = route < live && local >= 0 && local < p.sort.local_experts;
+    p.sort.expanded_to_permuted[route] = visible ? static_cast<int32_t>(route) : -1;
+  }
+}
+
 }  // namespace
+
+bool split_front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top) {
+  return tokens >= 1 && tokens <= kSplitMaxTokens && experts >= 1 && experts <= front_token::kMaxExperts &&
+         hidden % front_token::kChunk == 0 && hidden / front_token::kChunk <= 8 && top >= 1 &&
+         top <= topk::kHalf && top <= experts;
+}
+
+void launch_split_front(const FrontParams &p, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(ceil_div<int64_t>(p.experts, kSplitWaves)));
+  const int quant = p.hidden_codes == nullptr ? 0 : (p.hidden_mx_scales != nullptr ? 2 : 1);
+  const bool narrow = p.hidden <= 4 * front_token::kChunk;
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kSplitThreads), 0, stream, p); };
+  if (narrow && quant == 0) go(split_front_kernel<4, 0>);
+  else if (narrow && quant == 1) go(split_front_kernel<4, 1>);
+  else if (narrow) go(split_front_kernel<4, 2>);
+  else if (quant == 0) go(split_front_kernel<8, 0>);
+  else if (quant == 1) go(split_front_kernel<8, 1>);
+  else go(split_front_kernel<8, 2>);
+}
 
 constexpr int64_t kLocalMinTokens = 32;
 

@@ -58,6 +58,12 @@ void launch_front(const FrontParams &p, hipStream_t stream);
 bool local_front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top);
 void launch_local_front(const FrontParams &p, hipStream_t stream);
 
+/// The same for at most 8 tokens: one expert per wavefront across ceil(experts / 4) workgroups,
+/// the last of which (counter word 1 of `ticket`) routes every token. At most 128 experts, the
+/// hidden size in whole 512-channel chunks up to 4096.
+bool split_front_fits(int64_t tokens, int64_t experts, int64_t hidden, int64_t top);
+void launch_split_front(const FrontParams &p, hipStream_t stream);
+
 /// The front end at prefill sizes (front_prefill.hip): router scores, topk and (with `codes`) the
 /// hidden rows' quantisation in one launch, one workgroup per 32 tokens.
 struct PrefillFrontParams {

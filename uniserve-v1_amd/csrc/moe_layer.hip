@@ -412,6 +412,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         }
         if (by_expert && local_front_fits(call->tokens, call->experts, call->hidden_size, call->top))
           launch_local_front(fp, s);
+        else if (by_expert && split_front_fits(call->tokens, call->experts, call->hidden_size, call->top))
+          launch_split_front(fp, s);
         else
           launch_front(fp, s);
         if (int32_t status = launched(call, "router, topk and sort")) return status;
