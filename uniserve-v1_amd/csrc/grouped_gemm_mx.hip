@@ -183,9 +183,11 @@ __device__ __forceinline__ floatx4 mfma_mx(const u32x4 &a, const intx8 &b, uint3
 /// partial sums meeting in LDS in wave order - for batches too small to fill the chip otherwise.
 /// kByExpert: the rows are the routes naming the workgroup's local expert (FC1 reads token route /
 /// top, FC2 row `route`; both write row `route`), listed by the workgroup while its first weight
-/// chunk is in flight.
-template <bool kGated, bool kSplit, bool kByExpert = false>
+/// chunk is in flight. kRun (expert-major, unsplit): the workgroup serves kRun consecutive slices
+/// one after the other, listing the routes once (grid y = slices / kRun).
+template <bool kGated, bool kSplit, bool kByExpert = false, int kRun = 1>
 __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
+  static_assert(kRun == 1 || (kByExpert && !kSplit), "runs of slices: expert-major, unsplit");
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t route_count[kThreads / kWave + 1];
@@ -221,29 +223,37 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
 
   int64_t n0, n1;
   const int row_set = kSplit ? 0 : wave;
-  if constexpr (kGated) {
-    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 16 : 64) + row_set * 16;
-    n1 = p.out_width + n0;
-  } else {
-    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
-    n1 = n0 + 16;
-    if (!kByExpert && n0 >= p.out_width) return;  // (expert-major: whole slices only)
+  auto slice_rows = [&](int64_t slice) {
+    if constexpr (kGated) {
+      n0 = slice * (kSplit ? 16 : 64) + row_set * 16;
+      n1 = p.out_width + n0;
+    } else {
+      n0 = slice * (kSplit ? 32 : 128) + row_set * 32;
+      n1 = n0 + 16;
+    }
+  };
+  slice_rows(static_cast<int64_t>(blockIdx.y) * kRun);
+  if constexpr (!kGated && !kByExpert) {
+    if (n0 >= p.out_width) return;  // (expert-major: whole slices only)
   }
   const int64_t c_first = kSplit ? wave : 0;
   const int64_t c_step = kSplit ? kThreads / kWave : 1;
   // Weight lines: load i (0..3) of a chunk reads rows 8 (i % 2) + l / 8 of set i / 2, 16-byte piece
   // l % 8 of the row's 128-byte line. Lane l's A operand for MFMA h (row r16, K 128 h + 32 g ..)
   // is piece 4 h + g of row r16: gathered with ds_bpermute from load (r16 >= 8) of its set.
+  // This lane's weight scales: its row r16 of each set, two 4-byte stage words per chunk.
   const uint8_t *line_row[2];
-  line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
-  line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
+  const uint8_t *ws[2];
+  auto slice_pointers = [&]() {
+    line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
+    line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
+    ws[0] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n0 + r16) * p.ws_row;
+    ws[1] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n1 + r16) * p.ws_row;
+  };
+  slice_pointers();
   const bool upper = r16 >= 8;
   const int source0 = (r16 & 7) * 8 + g;  // piece g (MFMA h = 0)
   const int source1 = source0 + 4;        // piece g + 4 (MFMA h = 1)
-  // This lane's weight scales: its row r16 of each set, two 4-byte stage words per chunk.
-  const uint8_t *ws[2];
-  ws[0] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n0 + r16) * p.ws_row;
-  ws[1] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n1 + r16) * p.ws_row;
 
   // One chunk's operands: four weight lines, two 8-byte weight-scale words, and per token block
   // 64 activation bytes (two MFMAs' worth: pieces g and g + 4 of each 128-byte half) and an
@@ -269,6 +279,11 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     if (rows == 0) return;
   }
 
+  for (int run = 0; run < kRun; ++run) {
+  if (run > 0) {
+    slice_rows(static_cast<int64_t>(blockIdx.y) * kRun + run);
+    slice_pointers();
+  }
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint8_t *a[kPassTiles];
     const uint8_t *as[kPassTiles];
@@ -340,7 +355,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
         }
       }
     };
-    if (kByExpert && !kSplit && pass == 0) fetch_rest(c_first, cur);  // its lines went out before the scan
+    if (kByExpert && !kSplit && pass == 0 && run == 0) fetch_rest(c_first, cur);  // its lines went out before the scan
     else if (c_first < chunks) fetch(c_first, cur);
     for (int64_t c = c_first; c < chunks; c += 2 * c_step) {
       if (c + c_step < chunks) fetch(c + c_step, next);
@@ -384,6 +399,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
         store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
       }
     }
+  }
   }
 }
 
@@ -863,6 +879,12 @@ int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, vo
 
 namespace {
 
+/// FC2 (expert-major, unsplit): 128-row slices served per workgroup, one after the other. An
+/// MXFP4 FC2 slice is 48 KB of weights at 768 channels, too short a life for a workgroup: 30B
+/// T=64 FC2 31.5 us with one slice each, 30.0 with two, 28.0 with four, 36.3 with eight (FC1's
+/// 128 KB slices: 43.7 us alone, 49 in runs of two or four; the e4m3 FC2's 96 KB ones: no change).
+constexpr int kFc2Run = 4;
+
 void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_t stream) {
   p.ids = r.ids;
   p.live_tokens = r.live_tokens;
@@ -879,9 +901,16 @@ void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_
     else hipLaunchKernelGGL((stream_mx_kernel<false, true, true>), grid, dim3(kThreads), 0, stream, p);
     return;
   }
-  const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
-  if (gated) hipLaunchKernelGGL((stream_mx_kernel<true, false, true>), grid, dim3(kThreads), 0, stream, p);
-  else hipLaunchKernelGGL((stream_mx_kernel<false, false, true>), grid, dim3(kThreads), 0, stream, p);
+  if (gated) {
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
+    hipLaunchKernelGGL((stream_mx_kernel<true, false, true>), grid, dim3(kThreads), 0, stream, p);
+  } else if (slices % kFc2Run == 0) {
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices / kFc2Run));
+    hipLaunchKernelGGL((stream_mx_kernel<false, false, true, kFc2Run>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
+    hipLaunchKernelGGL((stream_mx_kernel<false, false, true>), grid, dim3(kThreads), 0, stream, p);
+  }
 }
 
 }  // namespace
