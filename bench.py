@@ -150,6 +150,38 @@ def measure(w, steps, warmup):
     return elapsed, kernel_ms
 
 
+def graph_timing(w, steps, calls=20):
+    """The same layer calls replayed from a captured HIP graph (`calls` per replay, at least three
+    replays): the device's own time per call, free of the host's per-call launch work. The first
+    two replays' outputs are checked against the eager call's, bit for bit."""
+    import torch
+
+    w.step()
+    torch.cuda.synchronize()
+    eager = w.out.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(calls):
+                w.step()
+    torch.cuda.synchronize()
+    replays = max(3, steps // calls)
+    for _ in range(2):
+        w.out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(w.out, eager):
+            raise RuntimeError("graph replay of the layer differs from the eager call")
+    start = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - start) / (replays * calls)
+
+
 def algorithmic(w):
     """Algorithmic bytes and flops of the layer and of FC1, from the run's own routing."""
     import torch
@@ -283,6 +315,7 @@ def traffic_summary(directory):
 def run_config(name, steps, warmup, with_cpu, cpu_runs):
     w = Workload(name)
     elapsed, kernel_ms = measure(w, steps, warmup)
+    graph_s = graph_timing(w, steps)
     alg = algorithmic(w)
     ms_per_step = elapsed / steps * 1e3
     tokens_per_s = w.tokens * steps / elapsed
@@ -309,6 +342,9 @@ def run_config(name, steps, warmup, with_cpu, cpu_runs):
         "touched_experts": alg["touched"],
         "route_gemm_us": round(kernel_ms["route_gemm"] * 1e3, 2),
         "gather_gemm_us": round(kernel_ms["gather_gemm"] * 1e3, 2),
+        # The same calls replayed from a HIP graph (not `value`: the eager calls are).
+        "graph_ms_per_step": round(graph_s * 1e3, 4),
+        "graph_tokens_per_s": round(w.tokens / graph_s, 1),
     }
     cpu = cpu_baseline(w, cpu_runs) if with_cpu else None
     return w, ms_per_step, tokens_per_s, roofline, layer, cpu

@@ -223,30 +223,33 @@ def test_tiny_config_against_the_fp32_oracle(device):
 
 
 @pytest.mark.parametrize("garbage", [1000, 3])
-def test_uncleared_front_counters_fail_loudly_then_clear(device, garbage):
+@pytest.mark.parametrize("tokens", [64, 1])
+def test_uncleared_front_counters_fail_loudly_then_clear(device, garbage, tokens):
     """A decode-size call whose workspace counters were not zero before it (a reused buffer): the
     output is NaN, not a quietly wrong result, the counters are cleared, and the next call is
     bit-for-bit the clean one. Garbage past the takers means no workgroup routes; garbage below it
     means a workgroup routes early (on the previous call's scores, here the same ones). The
-    workspace still holds the first call's maps, so no kernel reads outside its arrays either way."""
-    hidden, experts, top, intermediate, tokens = 2048, 128, 8, 768, 64
+    workspace still holds the first call's maps, so no kernel reads outside its arrays either way.
+    At 64 tokens the front end counts nothing (the words are only checked); at one token the
+    expert-split front end counts its workgroups on word 1."""
+    hidden, experts, top, intermediate = 2048, 128, 8, 768
     x = normal_bf16((tokens, hidden), 71, device=device)
     router = normal_bf16((experts, hidden), 72, 0.02, device)
     up_gate = normal_bf16((experts, 2 * intermediate, hidden), 73, 0.02, device)
     down = normal_bf16((experts, hidden, intermediate), 74, 0.02, device)
     layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens)
-    announce("front counters: clean call", garbage)
+    announce("front counters: clean call", garbage, tokens)
     clean = bf16_bits(layer(x, router, up_gate, down)).copy()
     ticket = layer.view("ticket", torch.int32, (256,))
     words = 1 + (tokens + 15) // 16
     assert (ticket[:words] == 0).all().item()
     ticket[:words] = garbage
-    announce("front counters: garbage before the call", garbage)
+    announce("front counters: garbage before the call", garbage, tokens)
     loud = layer(x, router, up_gate, down)
     torch.cuda.synchronize()
     assert torch.isnan(loud.float()).all().item()
     assert (ticket == 0).all().item()
-    announce("front counters: the call after", garbage)
+    announce("front counters: the call after", garbage, tokens)
     again = bf16_bits(layer(x, router, up_gate, down))
     assert np.array_equal(again, clean)
 
