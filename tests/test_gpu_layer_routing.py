@@ -49,6 +49,12 @@ ROUTED = {
     "bf16 8 tokens, map + load + window + live": (8, 2048, 128, 8, 768, "bf16", (16, 96), 6),
     "fp8 8 tokens, map + load + window": (8, 2048, 128, 8, 768, "f8e4m3", (16, 96), None),
     "mx 8 tokens, map + load + window": (8, 2048, 128, 8, 768, "f4e2m1", (16, 96), None),
+    # the expert-split front end (at most 8 tokens) off its usual shape: an expert count that is
+    # no multiple of its four experts per workgroup, one or three 512-channel chunks of a narrow
+    # row, five of a wide one, top 10
+    "fp8 5 tokens, 60 experts, 512 channels": (5, 512, 60, 4, 256, "f8e4m3", None, None),
+    "mx 3 tokens, 1536 channels, window + live": (3, 1536, 128, 8, 512, "f4e2m1", (8, 64), 2),
+    "bf16 7 tokens, 100 experts, top 10, 2560 channels": (7, 2560, 100, 10, 384, "bf16", None, None),
     # a window of 16 experts: 24 or more routes per local expert, so the decode front end (which
     # still quantises the hidden rows) hands over to the sort and the tiled products
     "fp8 decode, narrow window": (64, 2048, 128, 8, 768, "f8e4m3", (8, 16), None),
