@@ -118,8 +118,11 @@ constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is spli
 /// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
 /// kByExpert: workgroup x serves local expert x and lists its rows itself (the routes naming it in
 /// `ids`, route order), reading act row route / top (FC1) or route (FC2) and writing row `route`.
-template <bool kGated, bool kSplit, int kPassTiles, bool kByExpert = false>
+/// kRun (expert-major): the workgroup serves kRun consecutive slices one after the other, listing
+/// the routes once (grid y = slices / kRun).
+template <bool kGated, bool kSplit, int kPassTiles, bool kByExpert = false, int kRun = 1>
 __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p) {
+  static_assert(kRun == 1 || kByExpert, "runs of slices: expert-major");
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t route_count[kThreads / kWave + 1];
@@ -153,13 +156,18 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
 
   int64_t n0, n1;
   const int row_set = kSplit ? 0 : wave;
-  if constexpr (kGated) {
-    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 16 : 64) + row_set * 16;
-    n1 = p.out_width + n0;
-  } else {
-    n0 = static_cast<int64_t>(blockIdx.y) * (kSplit ? 32 : 128) + row_set * 32;
-    n1 = n0 + 16;
-    if (!kByExpert && n0 >= p.out_width) return;  // (expert-major: whole slices only)
+  auto slice_rows = [&](int64_t slice) {
+    if constexpr (kGated) {
+      n0 = slice * (kSplit ? 16 : 64) + row_set * 16;
+      n1 = p.out_width + n0;
+    } else {
+      n0 = slice * (kSplit ? 32 : 128) + row_set * 32;
+      n1 = n0 + 16;
+    }
+  };
+  slice_rows(static_cast<int64_t>(blockIdx.y) * kRun);
+  if constexpr (!kGated && !kByExpert) {
+    if (n0 >= p.out_width) return;  // (expert-major: whole slices only)
   }
   const int64_t kb_first = kSplit ? wave : 0;
   const int64_t kb_step = kSplit ? kThreads / kWave : 1;
@@ -169,13 +177,17 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   // chunks g and g + 4) is gathered from those loads with ds_bpermute; the activations use the
   // same K mapping.
   const uint8_t *line_row[2];
-  line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * p.K + (lane & 7) * 16;
-  line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * p.K + (lane & 7) * 16;
+  const float *ws0, *ws1;
+  auto slice_pointers = [&]() {
+    line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * p.K + (lane & 7) * 16;
+    line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * p.K + (lane & 7) * 16;
+    ws0 = p.weight_scales + (expert * (p.n_total / 128) + n0 / 128) * kb_count;
+    ws1 = p.weight_scales + (expert * (p.n_total / 128) + n1 / 128) * kb_count;
+  };
+  slice_pointers();
   const bool upper = r16 >= 8;
   const int source_lo = (r16 & 7) * 8 + g;  // chunk g of row r16
   const int source_hi = source_lo + 4;      // chunk g + 4
-  const float *ws0 = p.weight_scales + (expert * (p.n_total / 128) + n0 / 128) * kb_count;
-  const float *ws1 = p.weight_scales + (expert * (p.n_total / 128) + n1 / 128) * kb_count;
 
   // Expert-major: the first weight block goes out before the route scan (it depends on nothing the
   // routes decide), then the scan lists the expert's rows.
@@ -193,6 +205,11 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     if (rows == 0) return;
   }
 
+  for (int run = 0; run < kRun; ++run) {
+  if (run > 0) {
+    slice_rows(static_cast<int64_t>(blockIdx.y) * kRun + run);
+    slice_pointers();
+  }
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
     const uint8_t *a[kPassTiles];
     const float *as[kPassTiles];
@@ -326,7 +343,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     } else {
     intx8 acur[kPassTiles], anext[kPassTiles];
     float scur[2 + kPassTiles], snext[2 + kPassTiles];
-    if (kByExpert && pass == 0) {
+    if (kByExpert && pass == 0 && run == 0) {
       fetch_rest(kb_first, acur, scur);  // its weight lines went out before the route scan
     } else if (kb_first < kb_count) {
       fetch(kb_first, wcur, acur, scur);
@@ -374,6 +391,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
         store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
       }
     }
+  }
   }
 }
 
@@ -620,6 +638,11 @@ void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles
 
 bool fp8_stream_path(int64_t routes, int64_t experts) { return routes < kStreamRowsPerExpert * experts; }
 
+/// The split FC2 (few routes: 32-row slices, K over the waves): slices served per workgroup, one
+/// after the other (a 235B FC2 slice of 32 rows is 48 KB of weights): 235B T=1 FC2 17.7-18.3 ->
+/// 15.9 us by events with two (four: 23.2).
+constexpr int kSplitFc2Run = 2;
+
 void launch_expert_stream_fp8(const GroupedFp8Params &params, bool gated, int64_t local_experts, hipStream_t stream) {
   GroupedFp8Params p = params;
   p.local_experts = local_experts;
@@ -631,8 +654,12 @@ void launch_expert_stream_fp8(const GroupedFp8Params &params, bool gated, int64_
   const int64_t served = p.routes < local_experts ? p.routes : local_experts;
   if (served * slices < kSplitBelow) {
     const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(gated ? p.out_width / 16 : p.out_width / 32));
+    const dim3 run_grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(p.out_width / 32 / kSplitFc2Run));
+    const bool runs = !gated && (p.out_width / 32) % kSplitFc2Run == 0;
     if (gated && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
     else if (gated) hipLaunchKernelGGL((stream_fp8_kernel<true, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
+    else if (runs && one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 1, true, kSplitFc2Run>), run_grid, dim3(kThreads), 0, stream, p);
+    else if (runs) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2, true, kSplitFc2Run>), run_grid, dim3(kThreads), 0, stream, p);
     else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
     return;

@@ -183,11 +183,11 @@ __device__ __forceinline__ floatx4 mfma_mx(const u32x4 &a, const intx8 &b, uint3
 /// partial sums meeting in LDS in wave order - for batches too small to fill the chip otherwise.
 /// kByExpert: the rows are the routes naming the workgroup's local expert (FC1 reads token route /
 /// top, FC2 row `route`; both write row `route`), listed by the workgroup while its first weight
-/// chunk is in flight. kRun (expert-major, unsplit): the workgroup serves kRun consecutive slices
-/// one after the other, listing the routes once (grid y = slices / kRun).
+/// chunk is in flight. kRun (expert-major): the workgroup serves kRun consecutive slices one after
+/// the other, listing the routes once (grid y = slices / kRun).
 template <bool kGated, bool kSplit, bool kByExpert = false, int kRun = 1>
 __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
-  static_assert(kRun == 1 || (kByExpert && !kSplit), "runs of slices: expert-major, unsplit");
+  static_assert(kRun == 1 || kByExpert, "runs of slices: expert-major");
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t route_count[kThreads / kWave + 1];
@@ -884,6 +884,9 @@ namespace {
 /// T=64 FC2 31.5 us with one slice each, 30.0 with two, 28.0 with four, 36.3 with eight (FC1's
 /// 128 KB slices: 43.7 us alone, 49 in runs of two or four; the e4m3 FC2's 96 KB ones: no change).
 constexpr int kFc2Run = 4;
+/// The split FC2 (few routes: 32-row slices, K over the waves) likewise, two slices per workgroup:
+/// 235B T=1 FC2 14.2 -> 11.6 us by events (four: 15.9, eight: 23.2).
+constexpr int kSplitFc2Run = 2;
 
 void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_t stream) {
   p.ids = r.ids;
@@ -897,8 +900,14 @@ void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_
   const int64_t served = r.routes < r.local_experts ? r.routes : r.local_experts;
   if (served * slices < kSplitBelow) {
     const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(gated ? p.out_width / 16 : p.out_width / 32));
-    if (gated) hipLaunchKernelGGL((stream_mx_kernel<true, true, true>), grid, dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL((stream_mx_kernel<false, true, true>), grid, dim3(kThreads), 0, stream, p);
+    if (gated) {
+      hipLaunchKernelGGL((stream_mx_kernel<true, true, true>), grid, dim3(kThreads), 0, stream, p);
+    } else if ((p.out_width / 32) % kSplitFc2Run == 0) {
+      const dim3 run_grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(p.out_width / 32 / kSplitFc2Run));
+      hipLaunchKernelGGL((stream_mx_kernel<false, true, true, kSplitFc2Run>), run_grid, dim3(kThreads), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((stream_mx_kernel<false, true, true>), grid, dim3(kThreads), 0, stream, p);
+    }
     return;
   }
   if (gated) {
