@@ -157,9 +157,9 @@ __global__ void __launch_bounds__(kThreads) prefill_front_kernel(PrefillFrontPar
   issue(1);
   issue(2);
   for (int k = 0; k < stages; ++k) {
-    // Issued since stage k's loads: stages k + 1 and k + 2 (three loads each) and the stores of
+    // Issued since stage k's loads: stages k + 1 and k + 2 (kLoads loads each) and the stores of
     // the last min(k, 3) stages.
-    wait_vm(6 + stores * (k < 3 ? k : 3));
+    wait_vm(2 * kLoads + stores * (k < 3 ? k : 3));
     __syncthreads();
     issue(k + 3);
     // No memory access of the stage moves above its loads: the waits count this stage's stores

@@ -16,8 +16,8 @@
 //
 // Two product kernels, chosen by routes per expert as for the e4m3 products:
 //  * decode shapes: the stream kernel (one tile x a slice of weight rows per workgroup; weights
-//    streamed as whole 128-byte lines, non-temporal, and regrouped into the MFMA layout with
-//    ds_bpermute), walking K 256 elements (one 128-byte weight line) at a time;
+//    streamed as whole 128-byte lines, non-temporal, and regrouped into the MFMA layout through
+//    each wave's own LDS buffer), walking K 256 elements (one 128-byte weight line) at a time;
 //  * prefill shapes: the tiled kernel (one 128-row tile x 256 weight rows per workgroup, two
 //    workgroups per CU), both operands and both scale tables staged through LDS by DMA in two
 //    stages of 128 K.
@@ -158,15 +158,6 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
   *reinterpret_cast<uint2 *>(pointer) = packed;
 }
 
-/// The 16 bytes lane `source` holds in `value` (ds_bpermute).
-__device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
-  u32x4 out;
-#pragma unroll
-  for (int d = 0; d < 4; ++d)
-    out[d] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(source * 4, static_cast<int>(value[d])));
-  return out;
-}
-
 /// D += (E2M1 A scaled by 2^(sa - 127)) . (e4m3 B scaled by 2^(sb - 127)) over 128 K; the scales
 /// are this lane's bytes (its row and its 32 K elements).
 __device__ __forceinline__ floatx4 mfma_mx(const u32x4 &a, const intx8 &b, uint32_t sa, uint32_t sb, floatx4 c) {
@@ -191,6 +182,7 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t route_count[kThreads / kWave + 1];
+  __shared__ u32x4 regroup[kThreads / kWave][4 * 64];  // each wave's weight lines, regrouped
   int64_t expert, first;
   int rows = 0;
   if constexpr (kByExpert) {
@@ -240,20 +232,21 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   const int64_t c_step = kSplit ? kThreads / kWave : 1;
   // Weight lines: load i (0..3) of a chunk reads rows 8 (i % 2) + l / 8 of set i / 2, 16-byte piece
   // l % 8 of the row's 128-byte line. Lane l's A operand for MFMA h (row r16, K 128 h + 32 g ..)
-  // is piece 4 h + g of row r16: gathered with ds_bpermute from load (r16 >= 8) of its set.
-  // This lane's weight scales: its row r16 of each set, two 4-byte stage words per chunk.
-  const uint8_t *line_row[2];
-  const uint8_t *ws[2];
+  // is piece 4 h + g of row r16, regrouped through LDS. This lane's weight scales: its row r16 of
+  // each set, two 4-byte stage words per chunk. Every address is a uniform base (the expert's
+  // tables, the activation arrays) plus a 32-bit lane offset, so the loads take the scalar-base
+  // form and each address costs one VGPR.
+  expert = __builtin_amdgcn_readfirstlane(static_cast<int>(expert));
+  const uint8_t *wbase = p.weights + expert * p.n_total * weight_row_bytes;
+  const uint8_t *sbase = p.weight_scales + expert * p.n_total * scale_row_bytes;
+  uint32_t line_off[2], ws_off[2];
   auto slice_pointers = [&]() {
-    line_row[0] = p.weights + (expert * p.n_total + n0 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
-    line_row[1] = p.weights + (expert * p.n_total + n1 + lane / 8) * weight_row_bytes + (lane & 7) * 16;
-    ws[0] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n0 + r16) * p.ws_row;
-    ws[1] = p.weight_scales + expert * p.n_total * scale_row_bytes + (n1 + r16) * p.ws_row;
+    line_off[0] = static_cast<uint32_t>((n0 + lane / 8) * weight_row_bytes + (lane & 7) * 16);
+    line_off[1] = static_cast<uint32_t>((n1 + lane / 8) * weight_row_bytes + (lane & 7) * 16);
+    ws_off[0] = static_cast<uint32_t>((n0 + r16) * p.ws_row);
+    ws_off[1] = static_cast<uint32_t>((n1 + r16) * p.ws_row);
   };
   slice_pointers();
-  const bool upper = r16 >= 8;
-  const int source0 = (r16 & 7) * 8 + g;  // piece g (MFMA h = 0)
-  const int source1 = source0 + 4;        // piece g + 4 (MFMA h = 1)
 
   // One chunk's operands: four weight lines, two 8-byte weight-scale words, and per token block
   // 64 activation bytes (two MFMAs' worth: pieces g and g + 4 of each 128-byte half) and an
@@ -264,11 +257,12 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     intx8 x[kPassTiles][2];
     uint2 xscale[kPassTiles];
   };
+  const uint32_t row8 = static_cast<uint32_t>(8 * weight_row_bytes);
   auto fetch_lines = [&](int64_t c, Chunk &d) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       d.lines[i] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4 *>(line_row[i / 2] + static_cast<int64_t>(i % 2) * 8 * weight_row_bytes + c * 128));
+          reinterpret_cast<const u32x4 *>(wbase + (line_off[i / 2] + (i % 2) * row8 + static_cast<uint32_t>(c) * 128u)));
   };
   Chunk cur, next;
   if constexpr (kByExpert) {
@@ -285,8 +279,9 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     slice_pointers();
   }
   for (int pass = 0; pass < rows; pass += 16 * kPassTiles) {
-    const uint8_t *a[kPassTiles];
-    const uint8_t *as[kPassTiles];
+    uint32_t a_off[kPassTiles];
+    uint32_t as_off[kPassTiles];
+    const uint32_t as_stage = static_cast<uint32_t>(p.as_stage);
     bool valid[kPassTiles];
 #pragma unroll
     for (int ms = 0; ms < kPassTiles; ++ms) {
@@ -300,8 +295,8 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
         source = valid[ms] ? p.permuted_to_expanded[first + m] / p.top : 0;
       }
       if (!valid[ms]) source = 0;
-      a[ms] = p.act + source * p.K + g * 16;
-      as[ms] = p.act_scales + (p.as_by_route ? first + (valid[ms] ? m : 0) : source) * p.as_row;
+      a_off[ms] = static_cast<uint32_t>(source * p.K + g * 16);
+      as_off[ms] = static_cast<uint32_t>((p.as_by_route ? first + (valid[ms] ? m : 0) : source) * p.as_row);
     }
     floatx4 acc[2][kPassTiles];
 #pragma unroll
@@ -312,23 +307,23 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     auto fetch_rest = [&](int64_t c, Chunk &d) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        d.wscale[s] = uint2{*reinterpret_cast<const uint32_t *>(ws[s] + 2 * c * p.ws_stage),
-                            *reinterpret_cast<const uint32_t *>(ws[s] + (2 * c + 1) * p.ws_stage)};
+        d.wscale[s] = uint2{*reinterpret_cast<const uint32_t *>(sbase + (ws_off[s] + 2u * static_cast<uint32_t>(c) * static_cast<uint32_t>(p.ws_stage))),
+                            *reinterpret_cast<const uint32_t *>(sbase + (ws_off[s] + (2u * static_cast<uint32_t>(c) + 1u) * static_cast<uint32_t>(p.ws_stage)))};
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           if (valid[ms]) {
-            const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + c * 256 + h * 128);
-            const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + c * 256 + h * 128 + 64);
+            const u32x4 lo = *reinterpret_cast<const u32x4 *>(p.act + (a_off[ms] + static_cast<uint32_t>(c) * 256u + h * 128u));
+            const u32x4 hi = *reinterpret_cast<const u32x4 *>(p.act + (a_off[ms] + static_cast<uint32_t>(c) * 256u + h * 128u + 64u));
             d.x[ms][h] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                                static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
           } else {
             d.x[ms][h] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
           }
         }
-        d.xscale[ms] = valid[ms] ? uint2{*reinterpret_cast<const uint32_t *>(as[ms] + 2 * c * p.as_stage),
-                                         *reinterpret_cast<const uint32_t *>(as[ms] + (2 * c + 1) * p.as_stage)}
+        d.xscale[ms] = valid[ms] ? uint2{*reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + 2u * static_cast<uint32_t>(c) * as_stage)),
+                                         *reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + (2u * static_cast<uint32_t>(c) + 1u) * as_stage))}
                                  : uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
       }
     };
@@ -339,15 +334,20 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     // Byte 4 h + g of an 8-byte scale word: this lane's block of MFMA h.
     auto scale_byte = [&](const uint2 &word, int h) -> uint32_t { return ((h == 0 ? word.x : word.y) >> (8 * g)) & 0xffu; };
     auto compute = [&](const Chunk &d) {
+      // The four lines go through the wave's own LDS buffer into the operand layout: load i's lane
+      // l (row 8 (i % 2) + l / 8 of set i / 2, piece l % 8) at slot 64 i + 8 r + (piece ^ r), r = l / 8,
+      // so the 16 lanes that read one piece of 8 rows read 8 different bank groups.
+      {
+        const int row = lane >> 3, piece = lane & 7;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) regroup[wave][i * 64 + row * 8 + (piece ^ row)] = d.lines[i];
+      }
 #pragma unroll
       for (int set = 0; set < 2; ++set) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          // Every lane takes part in both permutes; the select picks its row's load.
-          const int source = h == 0 ? source0 : source1;
-          const u32x4 from_lo = permute16(source, d.lines[2 * set]);
-          const u32x4 from_hi = permute16(source, d.lines[2 * set + 1]);
-          const u32x4 w = upper ? from_hi : from_lo;
+          const int rr = r16 & 7, q = 4 * h + g;
+          const u32x4 w = regroup[wave][(2 * set + (r16 >> 3)) * 64 + rr * 8 + (q ^ rr)];
           const uint32_t sw = scale_byte(d.wscale[set], h);
 #pragma unroll
           for (int ms = 0; ms < kPassTiles; ++ms)
