@@ -100,15 +100,6 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
 /// re-streams its weights per pass, which at such averages is rare).
 constexpr int64_t kOnePassRowsPerExpert = 8;
 
-/// The 16 bytes lane `source` holds in `value`, gathered by this lane (ds_bpermute: lanes exchange
-/// registers without LDS allocation).
-__device__ __forceinline__ u32x4 permute16(int source, const u32x4 &value) {
-  u32x4 out;
-#pragma unroll
-  for (int d = 0; d < 4; ++d)
-    out[d] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(source * 4, static_cast<int>(value[d])));
-  return out;
-}
 constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is split over the waves
 
 /// Decode-shaped: as the bf16 stream kernel, one 128-deep scale block per chunk. kSplit: the four
@@ -126,6 +117,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
   __shared__ int32_t route_count[kThreads / kWave + 1];
+  __shared__ u32x4 regroup[kThreads / kWave][4 * 64];  // each wave's weight lines of a block, regrouped
   int64_t expert, first;
   int rows = 0;
   if constexpr (kByExpert) {
@@ -174,8 +166,11 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   // Weight lines: load i (0..3) of a scale block reads rows 8 (i % 2) + l / 8 of set i / 2 (set 0 =
   // rows n0.., set 1 = rows n1..), 16-byte chunk l % 8 - whole 128-byte lines, non-temporal (each
   // weight line is read once per call). Lane l's MFMA operand (row r16, 32 K bytes of group g:
-  // chunks g and g + 4) is gathered from those loads with ds_bpermute; the activations use the
-  // same K mapping.
+  // chunks g and g + 4) is gathered from those loads through the wave's own LDS buffer (load i's
+  // lane l, row l / 8 of the load and chunk l % 8, at slot 64 i + 8 r + (chunk ^ r), r = l / 8: the
+  // lanes reading one chunk of eight rows read eight bank groups); the activations use the same K
+  // mapping. (Against ds_bpermute from both candidate loads and a select: 30B T=64 FC2 42 -> 40 us,
+  // the layer 131 -> 127.)
   const uint8_t *line_row[2];
   const float *ws0, *ws1;
   auto slice_pointers = [&]() {
@@ -185,9 +180,6 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     ws1 = p.weight_scales + (expert * (p.n_total / 128) + n1 / 128) * kb_count;
   };
   slice_pointers();
-  const bool upper = r16 >= 8;
-  const int source_lo = (r16 & 7) * 8 + g;  // chunk g of row r16
-  const int source_hi = source_lo + 4;      // chunk g + 4
 
   // Expert-major: the first weight block goes out before the route scan (it depends on nothing the
   // routes decide), then the scan lists the expert's rows.
@@ -260,15 +252,16 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     };
     auto compute = [&](const u32x4 (&lines)[4], const intx8 (&x)[kPassTiles], const float (&s)[2 + kPassTiles]) {
       intx8 w[2];
+      {
+        const int row = lane >> 3, piece = lane & 7;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) regroup[wave][i * 64 + row * 8 + (piece ^ row)] = lines[i];
+      }
 #pragma unroll
       for (int set = 0; set < 2; ++set) {
-        // Every lane takes part in both permutes of both loads; the select picks its row's load.
-        const u32x4 lo0 = permute16(source_lo, lines[2 * set]);
-        const u32x4 lo1 = permute16(source_lo, lines[2 * set + 1]);
-        const u32x4 hi0 = permute16(source_hi, lines[2 * set]);
-        const u32x4 hi1 = permute16(source_hi, lines[2 * set + 1]);
-        const u32x4 lo = upper ? lo1 : lo0;
-        const u32x4 hi = upper ? hi1 : hi0;
+        const int i = 2 * set + (r16 >> 3), rr = r16 & 7;
+        const u32x4 lo = regroup[wave][i * 64 + rr * 8 + (g ^ rr)];
+        const u32x4 hi = regroup[wave][i * 64 + rr * 8 + ((g + 4) ^ rr)];
         w[set] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                        static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
       }
@@ -315,12 +308,14 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
           }
         };
         auto compute1 = [&](const Block &d) {
-          const u32x4 lo0 = permute16(source_lo, d.w[0]);
-          const u32x4 lo1 = permute16(source_lo, d.w[1]);
-          const u32x4 hi0 = permute16(source_hi, d.w[0]);
-          const u32x4 hi1 = permute16(source_hi, d.w[1]);
-          const u32x4 lo = upper ? lo1 : lo0;
-          const u32x4 hi = upper ? hi1 : hi0;
+          {
+            const int row = lane >> 3, piece = lane & 7;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) regroup[wave][i * 64 + row * 8 + (piece ^ row)] = d.w[i];
+          }
+          const int rr = r16 & 7, li = r16 >> 3;
+          const u32x4 lo = regroup[wave][li * 64 + rr * 8 + (g ^ rr)];
+          const u32x4 hi = regroup[wave][li * 64 + rr * 8 + ((g + 4) ^ rr)];
           const intx8 w = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                                 static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
 #pragma unroll
