@@ -109,7 +109,9 @@ __global__ void __launch_bounds__(kCombineThreads) combine_kernel(CombineParams 
   if (p.ticket != nullptr && __syncthreads_or(ticket_word != 0u)) {
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) sum[j] = __builtin_nanf("");
-    if (blockIdx.x == 0 && blockIdx.y == 0 && static_cast<int>(threadIdx.x) < p.ticket_words)
+    // The last workgroup dispatched clears the words, at its end: every other workgroup was
+    // dispatched before it and read them with its first instruction, so none can see them cleared.
+    if (blockIdx.x == gridDim.x - 1 && blockIdx.y == gridDim.y - 1 && static_cast<int>(threadIdx.x) < p.ticket_words)
       store_device(p.ticket + threadIdx.x, 0u);
   }
   Element result[kPerLane];
