@@ -191,6 +191,36 @@ def test_decode_front_quantises_like_the_mxfp8_quantiser(device, tokens, hidden,
     np.testing.assert_array_equal(got_s, want_s.cpu().numpy())
 
 
+@pytest.mark.parametrize("tokens,window", [(64, None), (64, (16, 64)), (200, None)])
+def test_decode_fc1_quantises_like_the_mxfp8_quantiser(device, tokens, window):
+    """At decode sizes (no sort) the MX FC1 also writes the gated rows as FC2's MXFP8 operand: the
+    codes and row-major E8M0 bytes of every visible route's row equal the stand-alone MXFP8
+    quantiser's of the bf16 gated rows the same launch leaves, bit for bit (rows scaled by powers
+    of two so that blocks span many exponents)."""
+    announce("decode mx FC1 quantisation", tokens, window)
+    experts, top, hidden, intermediate = 128, 8, 2048, 768
+    x, router, host_w = mx_layer_inputs(device, tokens, hidden, experts, intermediate, 120 + tokens)
+    x[::3] *= 2.0**20
+    x[1::5] *= 2.0**-30
+    w1, s1, w2, s2 = on(device, host_w)
+    if window is not None:
+        w1, s1 = w1[window[0]:window[0] + window[1]].contiguous(), s1[window[0]:window[0] + window[1]].contiguous()
+        w2, s2 = w2[window[0]:window[0] + window[1]].contiguous(), s2[window[0]:window[0] + window[1]].contiguous()
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f4e2m1")
+    layer(x, router, w1, w2, up_gate_scales=s1, down_scales=s2, window=window)
+    routes = tokens * top
+    e2p = layer.view("expanded_to_permuted", torch.int32, (routes,)).cpu().numpy()
+    visible = np.nonzero(e2p >= 0)[0]
+    assert 0 < visible.size and (window is not None or visible.size == routes)
+    gated = layer.view("gated", torch.bfloat16, (routes, intermediate)).clone()
+    want_q, want_s = ops.quantize_mxfp8(gated)
+    torch.cuda.synchronize()
+    got_q = layer.view("gated_q", torch.uint8, (routes, intermediate)).cpu().numpy()
+    got_s = layer.view("gated_s", torch.uint8, (routes, intermediate // 32)).cpu().numpy()
+    np.testing.assert_array_equal(got_q[visible], want_q.cpu().numpy()[visible])
+    np.testing.assert_array_equal(got_s[visible], want_s.cpu().numpy()[visible])
+
+
 def sampled_mx_layer(x_bits, ids, weights, host_w, experts, top):
     """The oracle's MX products and combine for a sample of tokens with given routes."""
     tokens = x_bits.shape[0]

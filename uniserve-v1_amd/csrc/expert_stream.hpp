@@ -39,8 +39,13 @@ struct ExpertRouting {
   int64_t routes, top, local_offset, local_experts;
 };
 
+/// With `codes` (and `code_scales`), FC1 also writes the gated rows as FC2's MXFP8 operand (codes
+/// [routes, width / 2], row-major E8M0 bytes [routes, width / 64]) - only where
+/// mx_fc1_quantizes_by_expert holds (the unsplit kernel, whose workgroups own whole 32-column
+/// blocks).
+bool mx_fc1_quantizes_by_expert(const ExpertRouting &r, int64_t width);
 void gather_gemm_mx_by_expert(const uniserve_gather_mx_call *call, const ExpertRouting &r, int32_t activation,
-                              void *stream);
+                              void *stream, uint8_t *codes = nullptr, uint8_t *code_scales = nullptr);
 void route_gemm_mx_by_expert(const uniserve_route_mx_call *call, const ExpertRouting &r, void *stream);
 
 }  // namespace uniserve

@@ -176,8 +176,14 @@ __device__ __forceinline__ floatx4 mfma_mx(const u32x4 &a, const intx8 &b, uint3
 /// top, FC2 row `route`; both write row `route`), listed by the workgroup while its first weight
 /// chunk is in flight. kRun (expert-major): the workgroup serves kRun consecutive slices one after
 /// the other, listing the routes once (grid y = slices / kRun).
-template <bool kGated, bool kSplit, bool kByExpert = false, int kRun = 1>
+/// kQuantOut (expert-major FC1, unsplit): the gated rows also leave as FC2's MXFP8 operand - the
+/// workgroup's 64 columns are two whole 32-column blocks, staged through LDS as the bf16 values the
+/// quantiser would read, then quantised by its routine (codes [routes, out_width] at out_codes,
+/// row-major E8M0 bytes [routes, out_width / 32] at out_code_scales).
+template <bool kGated, bool kSplit, bool kByExpert = false, int kRun = 1, bool kQuantOut = false>
 __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
+  static_assert(!kQuantOut || (kGated && !kSplit && kByExpert && kRun == 1), "MXFP8 out: expert-major FC1");
+  __shared__ uint16_t gated_tile[kQuantOut ? 16 * 64 : 1];
   static_assert(kRun == 1 || kByExpert, "runs of slices: expert-major");
   __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
@@ -394,10 +400,37 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = gate(acc[1][ms][i], p.activation) * acc[0][ms][i];
         store_bf16x4(row + n0 + 4 * g, v);
+        if constexpr (kQuantOut) {
+          uint2 packed;
+          packed.x = pack_bf16x2(v[0], v[1]);
+          packed.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<uint2 *>(gated_tile + r16 * 64 + wave * 16 + 4 * g) = packed;
+        }
       } else {
         store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
         store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
       }
+    }
+    if constexpr (kQuantOut) {
+      // The tile's 16 rows x two 32-column blocks, four lanes a block (the first two waves).
+      __syncthreads();
+      const int t = static_cast<int>(threadIdx.x);
+      const int r = t / 8, block = (t / 4) & 1, sub = t & 3;
+      const int m = pass + r;
+      if (t < 128 && m < rows) {
+        const u32x4 bits = *reinterpret_cast<const u32x4 *>(gated_tile + r * 64 + block * 32 + sub * 8);
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[2 * j] = __uint_as_float(bits[j] << 16);
+          v[2 * j + 1] = __uint_as_float(bits[j] & 0xffff0000u);
+        }
+        const int64_t route = listed(m);
+        const int64_t column = static_cast<int64_t>(blockIdx.y) * 64 + block * 32;
+        const uint32_t scale = mxfp8_eight(v, p.out_codes + route * p.out_width + column + sub * 8);
+        if (sub == 0) p.out_code_scales[route * (p.out_width / 32) + column / 32] = static_cast<uint8_t>(scale);
+      }
+      __syncthreads();
     }
   }
   }
@@ -910,7 +943,10 @@ void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_
     }
     return;
   }
-  if (gated) {
+  if (gated && p.out_codes != nullptr) {
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
+    hipLaunchKernelGGL((stream_mx_kernel<true, false, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
+  } else if (gated) {
     const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));
     hipLaunchKernelGGL((stream_mx_kernel<true, false, true>), grid, dim3(kThreads), 0, stream, p);
   } else if (slices % kFc2Run == 0) {
@@ -924,8 +960,13 @@ void launch_expert_mx(MxParams p, bool gated, const ExpertRouting &r, hipStream_
 
 }  // namespace
 
+bool mx_fc1_quantizes_by_expert(const ExpertRouting &r, int64_t width) {
+  const int64_t served = r.routes < r.local_experts ? r.routes : r.local_experts;
+  return served * (width / 2 / 64) >= kSplitBelow;
+}
+
 void gather_gemm_mx_by_expert(const uniserve_gather_mx_call *call, const ExpertRouting &r, int32_t activation,
-                              void *stream) {
+                              void *stream, uint8_t *codes, uint8_t *code_scales) {
   MxParams p{};
   p.act = static_cast<const uint8_t *>(call->hidden);
   p.act_scales = call->hidden_scales;
@@ -937,6 +978,8 @@ void gather_gemm_mx_by_expert(const uniserve_gather_mx_call *call, const ExpertR
   p.out_width = call->width / 2;
   p.top = call->top;
   p.activation = activation;
+  p.out_codes = codes;
+  p.out_code_scales = code_scales;
   scale_strides(call->weight_scale_layout, p.n_total, p.K, &p.ws_stage, &p.ws_row);
   scale_strides(UNISERVE_MX_SCALES_ROW_MAJOR, 0, p.K, &p.as_stage, &p.as_row);
   launch_expert_mx(p, true, r, static_cast<hipStream_t>(stream));

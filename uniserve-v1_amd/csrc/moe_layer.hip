@@ -227,9 +227,14 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   fc1.out_dtype = UNISERVE_DTYPE_BF16;
   fc1.multiprocessors = call->multiprocessors;
   fc1.weight_scale_layout = call->weight_scale_layout;
+  // Decode sizes on the unsplit kernel: FC1 also writes FC2's MXFP8 operand (QUANTIZE_GATED then
+  // launches nothing).
+  const bool fc1_quantizes = by_expert != nullptr && mx_fc1_quantizes_by_expert(*by_expert, 2 * call->intermediate);
   if (!want(UNISERVE_MOE_LAYER_GATHER)) {
   } else if (by_expert != nullptr) {
-    gather_gemm_mx_by_expert(&fc1, *by_expert, static_cast<int32_t>(call->activation), stream);
+    gather_gemm_mx_by_expert(&fc1, *by_expert, static_cast<int32_t>(call->activation), stream,
+                             fc1_quantizes ? static_cast<uint8_t *>(at(v.gated_q)) : nullptr,
+                             fc1_quantizes ? static_cast<uint8_t *>(at(v.gated_s)) : nullptr);
     if (int32_t status = launched(call, "gather_gemm_mx")) return status;
   } else if (gather_gemm_mx(&fc1, scale_rows, static_cast<int32_t>(call->activation), stream,
                             scale_rows != 0 ? static_cast<uint8_t *>(at(v.gated_q)) : nullptr,
@@ -247,8 +252,9 @@ int32_t run_mx_products(const uniserve_moe_layer_call *call, const uniserve_moe_
   qg.rows = by_expert != nullptr ? by_expert->routes : v.permuted_rows;
   qg.width = call->intermediate;
   qg.input_dtype = UNISERVE_DTYPE_BF16;
-  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) || scale_rows != 0) {
-    // (With route-major scales FC1 wrote the quantised rows itself.)
+  if (!want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) || scale_rows != 0 || fc1_quantizes) {
+    // (With route-major scales, or at decode sizes on the unsplit kernel, FC1 wrote the quantised
+    // rows itself.)
   } else if (uniserve_quantize_mxfp8(&qg, stream) != 0) {
     return forward_error(call, "quantize_mxfp8", qg);
   }
