@@ -84,9 +84,9 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
 // ---- stream kernel (decode) ----------------------------------------------------------------------------
 
 /// Average routes per expert at or below which the stream kernel takes a tile in passes of one
-/// 16-row MFMA block instead of two: 150 instead of 192 VGPRs, three waves per SIMD instead of
-/// two (FC2 at 64-token decode 68 vs 71.5 us); a tile with more rows re-streams its weights per
-/// pass, which at such averages is rare.
+/// 16-row MFMA block instead of two (at 64-token decode: FC2 63.7 against 66.2 us with two, FC1
+/// 124 against 125); a tile with more rows re-streams its weights per pass, which at such
+/// averages is rare.
 constexpr int64_t kOnePassRowsPerExpert = 8;
 
 //
@@ -216,7 +216,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
       for (int ms = 0; ms < kPassTiles; ++ms)
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          st.act[ms][s] = valid[ms] ? load16(a[ms] + offset + s * 32) : u32x4{0, 0, 0, 0};
+          st.act[ms][s] = load16(a[ms] + offset + s * 32);  // (rows past the tile: row 0, never stored)
     };
     auto load = [&](Stage &st, int64_t k) {
       load_lines(st, k);
@@ -242,11 +242,23 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
     };
     if (kByExpert && pass == 0) load_act(even, 0);  // its weight lines went out before the route scan
     else load(even, 0);
-    for (int k = 0; k < stages; k += 2) {
-      if (k + 1 < stages) load(odd, k + 1);
+    // The steady walk issues both loads unconditionally, so the compiler's wait before each
+    // compute counts exactly the other stage's loads still in flight (with the loads under
+    // conditions it waited for every load, the prefetched stage's too); the last one or two
+    // stages are peeled.
+    int k = 0;
+    for (; k + 2 < stages; k += 2) {
+      load(odd, k + 1);
       compute(even);
-      if (k + 2 < stages) load(even, k + 2);
-      if (k + 1 < stages) compute(odd);
+      load(even, k + 2);
+      compute(odd);
+    }
+    if (k + 1 < stages) {
+      load(odd, k + 1);
+      compute(even);
+      compute(odd);
+    } else {
+      compute(even);
     }
 
 #pragma unroll

@@ -96,8 +96,9 @@ __device__ __forceinline__ void store_bf16x4(uint16_t *pointer, floatx4 v) {
 }
 
 /// Average routes per expert at or below which the stream kernel takes a tile in passes of one
-/// 16-row MFMA block instead of two (fewer registers, more waves per SIMD; a tile with more rows
-/// re-streams its weights per pass, which at such averages is rare).
+/// 16-row MFMA block instead of two (fewer registers, more waves per SIMD: at 64-token decode FC1
+/// 63.6 against 66.4 us, FC2 35.8 against 39.2; a tile with more rows re-streams its weights per
+/// pass, which at such averages is rare).
 constexpr int64_t kOnePassRowsPerExpert = 8;
 
 constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is split over the waves
@@ -232,15 +233,11 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
       s[1] = ws1[kb];
 #pragma unroll
       for (int ms = 0; ms < kPassTiles; ++ms) {
-        if (valid[ms]) {
-          const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
-          const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
-          x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
-                        static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-        } else {
-          x[ms] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-        s[2 + ms] = valid[ms] ? as[ms][kb] : 0.0f;
+        const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
+        const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
+        x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                      static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+        s[2 + ms] = as[ms][kb];
       }
     };
     auto fetch = [&](int64_t kb, u32x4 (&w)[4], intx8 (&x)[kPassTiles], float (&s)[2 + kPassTiles]) {
@@ -277,8 +274,8 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     };
     if constexpr (kSplit) {
       // The split form walks its two 16-row sets one after the other: two weight lines per scale
-      // block in flight instead of four, so the kernel holds fewer registers (144 against 179) and
-      // three waves per SIMD instead of two - a single token's 768 workgroups (235B FC1) then run
+      // block in flight instead of four, so the kernel holds fewer registers and more waves per
+      // SIMD (measured when it was three against two) - a single token's 768 workgroups (235B FC1) then run
       // in one round (FC1 26 -> 22 us). At 64 tokens the unsplit kernel keeps both sets in flight
       // (walking them in turn there re-reads the activations: FC1 65 -> 77 us).
       struct Block {
@@ -296,15 +293,11 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
           d.s[0] = ws[kb];
 #pragma unroll
           for (int ms = 0; ms < kPassTiles; ++ms) {
-            if (valid[ms]) {
-              const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
-              const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
-              d.x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
-                              static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-            } else {
-              d.x[ms] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-            d.s[1 + ms] = valid[ms] ? as[ms][kb] : 0.0f;
+            const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
+            const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
+            d.x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                            static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+            d.s[1 + ms] = as[ms][kb];
           }
         };
         auto compute1 = [&](const Block &d) {
@@ -327,12 +320,23 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
           }
         };
         Block cur, next;
-        if (kb_first < kb_count) fetch1(kb_first, cur);
-        for (int64_t kb = kb_first; kb < kb_count; kb += 2 * kb_step) {
-          if (kb + kb_step < kb_count) fetch1(kb + kb_step, next);
-          compute1(cur);
-          if (kb + 2 * kb_step < kb_count) fetch1(kb + 2 * kb_step, cur);
-          if (kb + kb_step < kb_count) compute1(next);
+        // (Unconditional loads in the steady walk, the last blocks peeled: see the unsplit walk.)
+        int64_t kb = kb_first;
+        if (kb < kb_count) {
+          fetch1(kb, cur);
+          for (; kb + 2 * kb_step < kb_count; kb += 2 * kb_step) {
+            fetch1(kb + kb_step, next);
+            compute1(cur);
+            fetch1(kb + 2 * kb_step, cur);
+            compute1(next);
+          }
+          if (kb + kb_step < kb_count) {
+            fetch1(kb + kb_step, next);
+            compute1(cur);
+            compute1(next);
+          } else {
+            compute1(cur);
+          }
         }
       }
     } else {
@@ -343,11 +347,25 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     } else if (kb_first < kb_count) {
       fetch(kb_first, wcur, acur, scur);
     }
-    for (int64_t kb = kb_first; kb < kb_count; kb += 2 * kb_step) {
-      if (kb + kb_step < kb_count) fetch(kb + kb_step, wnext, anext, snext);
-      compute(wcur, acur, scur);
-      if (kb + 2 * kb_step < kb_count) fetch(kb + 2 * kb_step, wcur, acur, scur);
-      if (kb + kb_step < kb_count) compute(wnext, anext, snext);
+    // The steady walk issues both blocks' loads unconditionally, so the compiler's wait before
+    // each compute counts exactly the other block's loads still in flight (with the loads under
+    // conditions it waited for every load, the prefetched block's too); the last one or two
+    // blocks are peeled.
+    int64_t kb = kb_first;
+    if (kb < kb_count) {
+      for (; kb + 2 * kb_step < kb_count; kb += 2 * kb_step) {
+        fetch(kb + kb_step, wnext, anext, snext);
+        compute(wcur, acur, scur);
+        fetch(kb + 2 * kb_step, wcur, acur, scur);
+        compute(wnext, anext, snext);
+      }
+      if (kb + kb_step < kb_count) {
+        fetch(kb + kb_step, wnext, anext, snext);
+        compute(wcur, acur, scur);
+        compute(wnext, anext, snext);
+      } else {
+        compute(wcur, acur, scur);
+      }
     }
     }
     if constexpr (kSplit) {

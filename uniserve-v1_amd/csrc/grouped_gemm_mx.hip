@@ -99,7 +99,7 @@ __global__ void __launch_bounds__(kQuantThreads) quantize_mxfp8_kernel(MxQuantPa
 
 constexpr int kTileRows = 128;
 constexpr int kThreads = 256;
-constexpr int kPassTiles = 1;           // 16-token MFMA blocks per pass (one keeps two waves per SIMD)
+constexpr int kPassTiles = 1;           // 16-token MFMA blocks per pass (one keeps three waves per SIMD)
 constexpr int64_t kSplitBelow = 512;    // workgroups under which K is split over the waves
 
 struct MxParams {
@@ -319,18 +319,13 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
       for (int ms = 0; ms < kPassTiles; ++ms) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          if (valid[ms]) {
-            const u32x4 lo = *reinterpret_cast<const u32x4 *>(p.act + (a_off[ms] + static_cast<uint32_t>(c) * 256u + h * 128u));
-            const u32x4 hi = *reinterpret_cast<const u32x4 *>(p.act + (a_off[ms] + static_cast<uint32_t>(c) * 256u + h * 128u + 64u));
-            d.x[ms][h] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
-                               static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-          } else {
-            d.x[ms][h] = intx8{0, 0, 0, 0, 0, 0, 0, 0};
-          }
+          const u32x4 lo = *reinterpret_cast<const u32x4 *>(p.act + (a_off[ms] + static_cast<uint32_t>(c) * 256u + h * 128u));
+          const u32x4 hi = *reinterpret_cast<const u32x4 *>(p.act + (a_off[ms] + static_cast<uint32_t>(c) * 256u + h * 128u + 64u));
+          d.x[ms][h] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
+                             static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
         }
-        d.xscale[ms] = valid[ms] ? uint2{*reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + 2u * static_cast<uint32_t>(c) * as_stage)),
-                                         *reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + (2u * static_cast<uint32_t>(c) + 1u) * as_stage))}
-                                 : uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
+        d.xscale[ms] = uint2{*reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + 2u * static_cast<uint32_t>(c) * as_stage)),
+                             *reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + (2u * static_cast<uint32_t>(c) + 1u) * as_stage))};
       }
     };
     auto fetch = [&](int64_t c, Chunk &d) {
@@ -363,11 +358,25 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
     };
     if (kByExpert && !kSplit && pass == 0 && run == 0) fetch_rest(c_first, cur);  // its lines went out before the scan
     else if (c_first < chunks) fetch(c_first, cur);
-    for (int64_t c = c_first; c < chunks; c += 2 * c_step) {
-      if (c + c_step < chunks) fetch(c + c_step, next);
-      compute(cur);
-      if (c + 2 * c_step < chunks) fetch(c + 2 * c_step, cur);
-      if (c + c_step < chunks) compute(next);
+    // The steady walk issues both chunks' loads unconditionally, so the compiler's wait before
+    // each compute counts exactly the other chunk's loads still in flight (with the loads under
+    // conditions it waited for every load, the prefetched chunk's too); the last one or two
+    // chunks are peeled.
+    int64_t c = c_first;
+    if (c < chunks) {
+      for (; c + 2 * c_step < chunks; c += 2 * c_step) {
+        fetch(c + c_step, next);
+        compute(cur);
+        fetch(c + 2 * c_step, cur);
+        compute(next);
+      }
+      if (c + c_step < chunks) {
+        fetch(c + c_step, next);
+        compute(cur);
+        compute(next);
+      } else {
+        compute(cur);
+      }
     }
     if constexpr (kSplit) {
       // Waves 1..3 hand their partial sums to wave 0, which adds them in wave order.
