@@ -180,11 +180,16 @@ __global__ void __launch_bounds__(kSortThreads) small_sort_kernel(SortParams p) 
 constexpr int kSplitThreads = 512;
 constexpr int kSplitWaves = kSplitThreads / kWave;
 constexpr int64_t kSplitChunk = 2048;
+/// The layer's two-launch sort (counts in a scratch table, no parking) takes smaller chunks: four
+/// times the workgroups, each with a quarter of the serial count-and-place walk (30B T=8192: count
+/// 6.2 + scan-and-place 17.7 us against 7.3 + 20.0 with 2048-route chunks).
+constexpr int64_t kLayerChunk = 512;
 
+template <int64_t kChunkRoutes = kSplitChunk>
 __device__ __forceinline__ void split_chunk(const SortParams &p, int64_t *first, int64_t *past) {
-  const int64_t chunks = p.routes / kSplitChunk;
-  *first = static_cast<int64_t>(blockIdx.x) * kSplitChunk;
-  *past = static_cast<int64_t>(blockIdx.x) + 1 == chunks ? p.routes : *first + kSplitChunk;
+  const int64_t chunks = p.routes / kChunkRoutes;
+  *first = static_cast<int64_t>(blockIdx.x) * kChunkRoutes;
+  *past = static_cast<int64_t>(blockIdx.x) + 1 == chunks ? p.routes : *first + kChunkRoutes;
 }
 
 /// Per-wavefront counts of the held routes of [first, past): wavefront w takes the w-th contiguous
@@ -219,6 +224,7 @@ __device__ __forceinline__ void split_count(const SortParams &p, int64_t first, 
 
 /// `counts` null: each chunk's counts are parked at the head of its stretch of
 /// expanded_to_permuted (the entry's three-launch path); else they go to counts[chunk][E].
+template <int64_t kChunkRoutes>
 __global__ void __launch_bounds__(kSplitThreads) sort_count_kernel(SortParams p, int32_t *counts) {
   extern __shared__ int32_t lds[];
   const int E = p.local_experts;
@@ -227,7 +233,7 @@ __global__ void __launch_bounds__(kSplitThreads) sort_count_kernel(SortParams p,
   __syncthreads();
   const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
   int64_t first, past, slice_first, slice_past;
-  split_chunk(p, &first, &past);
+  split_chunk<kChunkRoutes>(p, &first, &past);
   split_count(p, first, past, live, wave_rows, &slice_first, &slice_past);
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kSplitThreads) {
@@ -368,37 +374,63 @@ __global__ void __launch_bounds__(kSplitThreads) sort_place_kernel(SortParams p)
 /// counts per expert (the totals) and those of the chunks before its own (its base in each
 /// expert), scans the experts' tiles, and places its chunk; workgroup 0 also writes the tile
 /// tables, the padding rows and the two counts. Every map entry as the three-launch path writes it.
+/// Parts each expert's column of the count table is read in (the workgroup's threads over
+/// experts x parts), and the LDS words of the kernel.
+__host__ __device__ inline int scan_place_parts(int64_t local_experts) {
+  return local_experts >= kSplitThreads ? 1 : static_cast<int>(kSplitThreads / local_experts);
+}
+inline size_t scan_place_lds_bytes(int64_t local_experts) {
+  return static_cast<size_t>((kSplitWaves + 3 + 2 * scan_place_parts(local_experts)) * local_experts) * sizeof(int32_t);
+}
+
+template <int64_t kChunkRoutes>
 __global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortParams p, const int32_t *counts) {
   extern __shared__ int32_t lds[];
   const int E = p.local_experts;
+  const int parts = scan_place_parts(E);
   int32_t *start = lds;              // [E] this chunk's first row in each expert
   int32_t *wave_rows = start + E;    // [kSplitWaves][E]
   int32_t *total = wave_rows + kSplitWaves * E;   // [E]
   int32_t *first_row = total + E;                 // [E]
+  int32_t *part_total = first_row + E;            // [parts][E]
+  int32_t *part_before = part_total + parts * E;  // [parts][E]
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const uint64_t below = (1ull << lane) - 1ull;
   const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
-  const int64_t chunks = p.routes / kSplitChunk;
+  const int64_t chunks = p.routes / kChunkRoutes;
   const int64_t own = blockIdx.x;
   constexpr int kBatchChunks = 16;
 
-  for (int e = threadIdx.x; e < E; e += kSplitThreads) {
+  // Each expert's column of counts in `parts` contiguous runs of chunks, one thread a run.
+  for (int i = threadIdx.x; i < E * parts; i += kSplitThreads) {
+    const int e = i % E, part = i / E;
+    const int64_t c_begin = chunks * part / parts, c_end = chunks * (part + 1) / parts;
     int32_t running = 0, before = 0;
-    for (int64_t c0 = 0; c0 < chunks; c0 += kBatchChunks) {
+    for (int64_t c0 = c_begin; c0 < c_end; c0 += kBatchChunks) {
       int32_t count[kBatchChunks];
 #pragma unroll
-      for (int u = 0; u < kBatchChunks; ++u) count[u] = c0 + u < chunks ? counts[(c0 + u) * E + e] : 0;
+      for (int u = 0; u < kBatchChunks; ++u) count[u] = c0 + u < c_end ? counts[(c0 + u) * E + e] : 0;
 #pragma unroll
       for (int u = 0; u < kBatchChunks; ++u) {
-        if (c0 + u == own) before = running;
+        if (c0 + u < own) before += count[u];
         running += count[u];
       }
+    }
+    part_total[part * E + e] = running;
+    part_before[part * E + e] = before;
+  }
+  for (int i = threadIdx.x; i < kSplitWaves * E; i += kSplitThreads) wave_rows[i] = 0;
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kSplitThreads) {
+    int32_t running = 0, before = 0;
+    for (int part = 0; part < parts; ++part) {
+      running += part_total[part * E + e];
+      before += part_before[part * E + e];
     }
     total[e] = running;
     start[e] = before;
   }
-  for (int i = threadIdx.x; i < kSplitWaves * E; i += kSplitThreads) wave_rows[i] = 0;
   __syncthreads();
 
   if (wave == 0) {
@@ -445,7 +477,7 @@ __global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortPara
   }
 
   int64_t first, past, slice_first, slice_past;
-  split_chunk(p, &first, &past);
+  split_chunk<kChunkRoutes>(p, &first, &past);
   split_count(p, first, past, live, wave_rows, &slice_first, &slice_past);
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kSplitThreads) {
@@ -484,15 +516,15 @@ bool layer_sort_two_launches(int64_t routes, int64_t local_experts) {
 }
 
 int64_t layer_sort_scratch_bytes(int64_t routes, int64_t local_experts) {
-  return routes / kSplitChunk * local_experts * static_cast<int64_t>(sizeof(int32_t));
+  return routes / kLayerChunk * local_experts * static_cast<int64_t>(sizeof(int32_t));
 }
 
 void launch_layer_sort(const sort::SortParams &p, int32_t *counts, hipStream_t stream) {
-  const uint32_t chunks = static_cast<uint32_t>(p.routes / kSplitChunk);
+  const uint32_t chunks = static_cast<uint32_t>(p.routes / kLayerChunk);
   const size_t count_bytes = kSplitWaves * p.local_experts * sizeof(int32_t);
-  hipLaunchKernelGGL(sort_count_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes, stream, p, counts);
-  hipLaunchKernelGGL(sort_scan_place_kernel, dim3(chunks), dim3(kSplitThreads),
-                     count_bytes + 3 * p.local_experts * sizeof(int32_t), stream, p, static_cast<const int32_t *>(counts));
+  hipLaunchKernelGGL((sort_count_kernel<kLayerChunk>), dim3(chunks), dim3(kSplitThreads), count_bytes, stream, p, counts);
+  hipLaunchKernelGGL((sort_scan_place_kernel<kLayerChunk>), dim3(chunks), dim3(kSplitThreads),
+                     scan_place_lds_bytes(p.local_experts), stream, p, static_cast<const int32_t *>(counts));
 }
 
 }  // namespace uniserve
@@ -553,7 +585,7 @@ extern "C" int32_t uniserve_moe_sort(const uniserve_moe_sort_call *call, void *s
     }
     const uint32_t chunks = static_cast<uint32_t>(p.routes / kSplitChunk);
     const size_t count_bytes = kSplitWaves * call->local_experts * sizeof(int32_t);
-    hipLaunchKernelGGL(sort_count_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes, s, p, nullptr);
+    hipLaunchKernelGGL((sort_count_kernel<kSplitChunk>), dim3(chunks), dim3(kSplitThreads), count_bytes, s, p, nullptr);
     hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kSortThreads), 2 * call->local_experts * sizeof(int32_t), s, p);
     hipLaunchKernelGGL(sort_place_kernel, dim3(chunks), dim3(kSplitThreads), count_bytes + call->local_experts * sizeof(int32_t),
                        s, p);
