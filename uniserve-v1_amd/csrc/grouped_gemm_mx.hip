@@ -324,8 +324,11 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
           d.x[ms][h] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
                              static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
         }
-        d.xscale[ms] = uint2{*reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + 2u * static_cast<uint32_t>(c) * as_stage)),
-                             *reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + (2u * static_cast<uint32_t>(c) + 1u) * as_stage))};
+        if constexpr (kByExpert)  // row-major activation scales: the chunk's two words are adjacent
+          d.xscale[ms] = *reinterpret_cast<const uint2 *>(p.act_scales + (as_off[ms] + 8u * static_cast<uint32_t>(c)));
+        else
+          d.xscale[ms] = uint2{*reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + 2u * static_cast<uint32_t>(c) * as_stage)),
+                               *reinterpret_cast<const uint32_t *>(p.act_scales + (as_off[ms] + (2u * static_cast<uint32_t>(c) + 1u) * as_stage))};
       }
     };
     auto fetch = [&](int64_t c, Chunk &d) {
