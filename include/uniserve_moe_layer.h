@@ -136,9 +136,10 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_
 ///   products take them route-major (views.route_scales);
 /// - otherwise each step launches its own operator.
 /// The quantiser steps launch nothing for bf16 weights, and QUANTIZE_GATED nothing where FC1
-/// writes its rows already quantised (e4m3 at prefill sizes; MXFP4 with route-major scales, and at
-/// decode sizes where the local experts with routes times intermediate / 64 reach 512 - 30B at 64
-/// tokens, not one token).
+/// writes its rows already quantised (e4m3 at prefill sizes; MXFP4 with route-major scales; and, for
+/// both e4m3 and MXFP4, at decode sizes where the local experts with routes times intermediate / 64
+/// reach 512 - 30B at 64 tokens, not one token - with an intermediate size of whole 128-column
+/// groups for e4m3).
 enum uniserve_moe_layer_step {
   UNISERVE_MOE_LAYER_ROUTER = 0,
   UNISERVE_MOE_LAYER_TOPK = 1,

@@ -320,6 +320,39 @@ def test_decode_front_quantises_like_the_quantiser(device, tokens, hidden, inter
     np.testing.assert_array_equal(got_s.view(np.uint32), want_s.cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("tokens,window", [(64, None), (64, (16, 64)), (200, None)])
+def test_decode_fc1_quantises_like_the_quantiser(device, tokens, window):
+    """At decode sizes (no sort) the e4m3 FC1 also writes the gated rows as FC2's operand: the codes
+    and scales of every visible route's row equal the stand-alone quantiser's of the bf16 gated
+    rows the same launch leaves, bit for bit (rows scaled by powers of two so that groups span
+    many exponents). 200 tokens take two 16-row passes per workgroup."""
+    announce("decode e4m3 FC1 quantisation", tokens, window)
+    experts, top, hidden, intermediate = 128, 8, 2048, 768
+    x, router, up_gate, down = layer_inputs(device, tokens, hidden, experts, intermediate, 130 + tokens)
+    x[::3] *= 2.0**20
+    x[1::5] *= 2.0**-30
+    q1, s1 = O.quantize_blocks_fp8(bf16_bits(up_gate))
+    q2, s2 = O.quantize_blocks_fp8(bf16_bits(down))
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    w1, ws1, w2, ws2 = d(q1), d(s1), d(q2), d(s2)
+    if window is not None:
+        w1, ws1 = w1[window[0]:window[0] + window[1]].contiguous(), ws1[window[0]:window[0] + window[1]].contiguous()
+        w2, ws2 = w2[window[0]:window[0] + window[1]].contiguous(), ws2[window[0]:window[0] + window[1]].contiguous()
+    layer = ops.MoeLayer(hidden, experts, top, intermediate, tokens, weight_dtype="f8e4m3")
+    layer(x, router, w1, w2, up_gate_scales=ws1, down_scales=ws2, window=window)
+    routes = tokens * top
+    e2p = layer.view("expanded_to_permuted", torch.int32, (routes,)).cpu().numpy()
+    visible = np.nonzero(e2p >= 0)[0]
+    assert 0 < visible.size and (window is not None or visible.size == routes)
+    gated = layer.view("gated", torch.bfloat16, (routes, intermediate)).clone()
+    want_q, want_s = ops.quantize_fp8(gated)
+    torch.cuda.synchronize()
+    got_q = layer.view("gated_q", torch.uint8, (routes, intermediate)).cpu().numpy()
+    got_s = layer.view("gated_s", torch.float32, (routes, intermediate // 128)).cpu().numpy()
+    np.testing.assert_array_equal(got_q[visible], want_q.cpu().numpy()[visible])
+    np.testing.assert_array_equal(got_s[visible].view(np.uint32), want_s.cpu().numpy()[visible].view(np.uint32))
+
+
 def test_prefill_fc1_quantises_like_the_quantiser(device):
     """At prefill shapes the layer's FC1 writes the gated rows straight in FC2's e4m3 form; codes
     and scales of every live row equal the stand-alone FC1 (bf16 out) followed by quantize_fp8."""

@@ -157,8 +157,11 @@ void launch_quantize_fp8(const void *input, bool input_f32, uint8_t *out, float 
 void launch_grouped_fp8(const GroupedFp8Params &p, bool gated, int64_t max_tiles, bool stream_path, bool one_pass,
                         hipStream_t stream);
 bool fp8_stream_path(int64_t routes, int64_t experts);
-/// The expert-major stream kernel over `local_experts` workgroup columns (p.ids .. set).
+/// The expert-major stream kernel over `local_experts` workgroup columns (p.ids .. set). FC1 with
+/// p.out_codes (only where expert_stream_fp8_fc1_quantizes holds: the unsplit kernel) also writes
+/// the gated rows as FC2's e4m3 operand (codes [routes, out_width], scales [routes, out_width / 128]).
 void launch_expert_stream_fp8(const GroupedFp8Params &p, bool gated, int64_t local_experts, hipStream_t stream);
+bool expert_stream_fp8_fc1_quantizes(int64_t routes, int64_t local_experts, int64_t out_width);
 
 /// The quantiser over token rows that also scatters each scale to the permuted rows of the
 /// token's routes: route_scales[g, expanded_to_permuted[t, k]] for every held route (k < top).

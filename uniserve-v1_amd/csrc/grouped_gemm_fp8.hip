@@ -112,13 +112,23 @@ constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is spli
 /// `ids`, route order), reading act row route / top (FC1) or route (FC2) and writing row `route`.
 /// kRun (expert-major): the workgroup serves kRun consecutive slices one after the other, listing
 /// the routes once (grid y = slices / kRun).
-template <bool kGated, bool kSplit, int kPassTiles, bool kByExpert = false, int kRun = 1>
-__global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p) {
+/// kWaves (unsplit): the workgroup's wavefronts, 16 gated columns each (FC1). kQuantOut (expert-major
+/// FC1, eight waves): the workgroup's 128 gated columns are one whole e4m3 scale group, so it also
+/// writes the gated rows as FC2's operand - staged in LDS as the bf16 values the quantiser would
+/// read, then quantised by its group routine (codes [routes, out_width] at out_codes, scales
+/// [routes, out_width / 128] at out_code_scales).
+template <bool kGated, bool kSplit, int kPassTiles, bool kByExpert = false, int kRun = 1, int kWaves = 4,
+          bool kQuantOut = false>
+__global__ void __launch_bounds__(kWaves * kWave) stream_fp8_kernel(GroupedFp8Params p) {
   static_assert(kRun == 1 || kByExpert, "runs of slices: expert-major");
-  __shared__ floatx4 partial[kSplit ? kThreads / kWave - 1 : 1][2][kPassTiles][kWave];
+  static_assert(kWaves == 4 || !kSplit, "the split form: four waves");
+  static_assert(!kQuantOut || (kGated && !kSplit && kByExpert && kWaves == 8), "e4m3 out: eight-wave FC1");
+  constexpr int kThreads = kWaves * kWave;
+  __shared__ floatx4 partial[kSplit ? kWaves - 1 : 1][2][kPassTiles][kWave];
   __shared__ int32_t route_list[kByExpert ? kExpertRoutes : 1];
-  __shared__ int32_t route_count[kThreads / kWave + 1];
-  __shared__ u32x4 regroup[kThreads / kWave][4 * 64];  // each wave's weight lines of a block, regrouped
+  __shared__ int32_t route_count[kWaves + 1];
+  __shared__ u32x4 regroup[kWaves][4 * 64];  // each wave's weight lines of a block, regrouped
+  __shared__ uint16_t gated_tile[kQuantOut ? 16 * kPassTiles * 128 : 1];
   int64_t expert, first;
   int rows = 0;
   if constexpr (kByExpert) {
@@ -139,7 +149,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     rows = p.tile_to_limit[tile] - static_cast<int>(first);
   }
   auto listed = [&](int m) -> int64_t {
-    return listed_route<kThreads / kWave>(route_list, route_count, p.routes, m);
+    return listed_route<kWaves>(route_list, route_count, p.routes, m);
   };
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
@@ -151,10 +161,10 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   const int row_set = kSplit ? 0 : wave;
   auto slice_rows = [&](int64_t slice) {
     if constexpr (kGated) {
-      n0 = slice * (kSplit ? 16 : 64) + row_set * 16;
+      n0 = slice * (kSplit ? 16 : kWaves * 16) + row_set * 16;
       n1 = p.out_width + n0;
     } else {
-      n0 = slice * (kSplit ? 32 : 128) + row_set * 32;
+      n0 = slice * (kSplit ? 32 : kWaves * 32) + row_set * 32;
       n1 = n0 + 16;
     }
   };
@@ -163,7 +173,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
     if (n0 >= p.out_width) return;  // (expert-major: whole slices only)
   }
   const int64_t kb_first = kSplit ? wave : 0;
-  const int64_t kb_step = kSplit ? kThreads / kWave : 1;
+  const int64_t kb_step = kSplit ? kWaves : 1;
   // Weight lines: load i (0..3) of a scale block reads rows 8 (i % 2) + l / 8 of set i / 2 (set 0 =
   // rows n0.., set 1 = rows n1..), 16-byte chunk l % 8 - whole 128-byte lines, non-temporal (each
   // weight line is read once per call). Lane l's MFMA operand (row r16, 32 K bytes of group g:
@@ -193,8 +203,8 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
   }
   if constexpr (kByExpert) {
     const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
-    rows = list_expert_routes<kThreads / kWave>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
-                                                route_list, route_count);
+    rows = list_expert_routes<kWaves>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
+                                      route_list, route_count);
     if (rows == 0) return;
   }
 
@@ -379,7 +389,7 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
       __syncthreads();
       if (wave == 0) {
 #pragma unroll
-        for (int w = 0; w < kThreads / kWave - 1; ++w)
+        for (int w = 0; w < kWaves - 1; ++w)
 #pragma unroll
           for (int set = 0; set < 2; ++set)
 #pragma unroll
@@ -399,10 +409,28 @@ __global__ void __launch_bounds__(kThreads) stream_fp8_kernel(GroupedFp8Params p
 #pragma unroll
         for (int i = 0; i < 4; ++i) h[i] = gate(acc[1][ms][i], p.activation) * acc[0][ms][i];
         store_bf16x4(row + n0 + 4 * g, h);
+        if constexpr (kQuantOut) {
+          uint2 packed;
+          packed.x = pack_bf16x2(h[0], h[1]);
+          packed.y = pack_bf16x2(h[2], h[3]);
+          *reinterpret_cast<uint2 *>(gated_tile + (ms * 16 + r16) * 128 + wave * 16 + 4 * g) = packed;
+        }
       } else {
         store_bf16x4(row + n0 + 4 * g, acc[0][ms]);
         store_bf16x4(row + n1 + 4 * g, acc[1][ms]);
       }
+    }
+    if constexpr (kQuantOut) {
+      // The pass's rows x the workgroup's 128 columns (one e4m3 group), 16 lanes a row.
+      __syncthreads();
+      const int t = static_cast<int>(threadIdx.x);
+      const int r = t / 16, m = pass + r;
+      if (r < 16 * kPassTiles && m < rows) {
+        const int64_t route = listed(m);
+        quantize_bf16_group(gated_tile + r * 128, p.out_codes + route * p.out_width + blockIdx.y * 128,
+                            p.out_code_scales + route * (p.out_width / 128) + blockIdx.y, t & 15);
+      }
+      __syncthreads();
     }
   }
   }
@@ -656,6 +684,11 @@ bool fp8_stream_path(int64_t routes, int64_t experts) { return routes < kStreamR
 /// 15.9 us by events with two (four: 23.2).
 constexpr int kSplitFc2Run = 2;
 
+bool expert_stream_fp8_fc1_quantizes(int64_t routes, int64_t local_experts, int64_t out_width) {
+  const int64_t served = routes < local_experts ? routes : local_experts;
+  return served * (out_width / 64) >= kSplitBelow && out_width % 128 == 0;
+}
+
 void launch_expert_stream_fp8(const GroupedFp8Params &params, bool gated, int64_t local_experts, hipStream_t stream) {
   GroupedFp8Params p = params;
   p.local_experts = local_experts;
@@ -675,6 +708,15 @@ void launch_expert_stream_fp8(const GroupedFp8Params &params, bool gated, int64_
     else if (runs) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2, true, kSplitFc2Run>), run_grid, dim3(kThreads), 0, stream, p);
     else if (one_pass) hipLaunchKernelGGL((stream_fp8_kernel<false, true, 1, true>), grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL((stream_fp8_kernel<false, true, 2, true>), grid, dim3(kThreads), 0, stream, p);
+    return;
+  }
+  if (gated && p.out_codes != nullptr) {
+    // The gated rows also as FC2's operand: eight-wave workgroups of 128 gated columns.
+    const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(p.out_width / 128));
+    if (one_pass)
+      hipLaunchKernelGGL((stream_fp8_kernel<true, false, 1, true, 1, 8, true>), grid, dim3(8 * kWave), 0, stream, p);
+    else
+      hipLaunchKernelGGL((stream_fp8_kernel<true, false, 2, true, 1, 8, true>), grid, dim3(8 * kWave), 0, stream, p);
     return;
   }
   const dim3 grid(static_cast<uint32_t>(columns), static_cast<uint32_t>(slices));

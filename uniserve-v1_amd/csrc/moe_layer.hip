@@ -593,8 +593,15 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         e.local_offset = call->local_offset;
         e.top = call->top;
         e.activation = activation;
+        // Where the unsplit kernel serves FC1 it also writes FC2's operand (QUANTIZE_GATED then
+        // launches nothing).
+        const bool fc1_quantizes = expert_stream_fp8_fc1_quantizes(routes, local_experts, call->intermediate);
         if (want(UNISERVE_MOE_LAYER_GATHER)) {
           GroupedFp8Params fc1 = e;
+          if (fc1_quantizes) {
+            fc1.out_codes = static_cast<uint8_t *>(at(v.gated_q));
+            fc1.out_code_scales = static_cast<float *>(at(v.gated_s));
+          }
           fc1.act = static_cast<const uint8_t *>(at(v.hidden_q));
           fc1.act_scales = static_cast<const float *>(at(v.hidden_s));
           fc1.weights = static_cast<const uint8_t *>(call->up_gate);
@@ -606,7 +613,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
           launch_expert_stream_fp8(fc1, true, local_experts, s);
           if (int32_t status = launched(call, "gather_gemm_fp8")) return status;
         }
-        if (want(UNISERVE_MOE_LAYER_QUANTIZE_GATED)) {
+        if (want(UNISERVE_MOE_LAYER_QUANTIZE_GATED) && !fc1_quantizes) {
           launch_quantize_fp8(at(v.gated), false, static_cast<uint8_t *>(at(v.gated_q)), static_cast<float *>(at(v.gated_s)),
                               nullptr, routes, call->intermediate, s);
           if (int32_t status = launched(call, "quantize_fp8")) return status;
