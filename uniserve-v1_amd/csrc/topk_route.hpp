@@ -101,6 +101,13 @@ __device__ __forceinline__ void max_step(float &maximum) {
 }
 
 template <int kOffset>
+__device__ __forceinline__ void max_key_step(uint64_t &key) {
+  const uint64_t other = (static_cast<uint64_t>(static_cast<uint32_t>(xor_lane<kOffset>(static_cast<int>(key >> 32)))) << 32) |
+                         static_cast<uint32_t>(xor_lane<kOffset>(static_cast<int>(static_cast<uint32_t>(key))));
+  key = key < other ? other : key;
+}
+
+template <int kOffset>
 __device__ __forceinline__ void sum_step(float &sum) {
   sum = sum + xor_lane<kOffset>(sum);
 }
@@ -167,6 +174,52 @@ __device__ __forceinline__ int32_t route(const void *scores, int score_kind, int
   // scores) names no expert: value -1, expert INT_MAX, as in the reference.
   float picked = 0.0f;
   int picked_expert = 0;
+  if constexpr (kIter <= 4) {
+    // The same selection on 64-bit keys (probability bits, then the complement of the expert id):
+    // a candidate's probability is >= 0, so its bits order as the values do, and among equal
+    // probabilities the lower id has the larger key - one unsigned maximum per round does the
+    // (value, lower id) arg-max. Non-candidates hold key 0, below every candidate's. Each lane
+    // sorts its keys once, largest first; a round's offer is the lane's first key not yet taken,
+    // and only the lane whose offer won moves on (keys are distinct: the ids are). Half the
+    // instructions of a round of the float butterfly and the ballots.
+    uint64_t key[kIter];
+#pragma unroll
+    for (int it = 0; it < kIter; ++it) {
+      const int expert = lane + it * kHalf;
+      const bool candidate = expert < experts && values[it] >= 0.0f;
+      key[it] = candidate ? (static_cast<uint64_t>(__float_as_uint(values[it])) << 32) | (~static_cast<uint32_t>(expert))
+                          : 0ull;
+    }
+    auto order = [&](int a, int b) {  // key[a] >= key[b] afterwards
+      const uint64_t x = key[a], y = key[b];
+      key[a] = x < y ? y : x;
+      key[b] = x < y ? x : y;
+    };
+    if constexpr (kIter >= 2) order(0, 1);
+    if constexpr (kIter == 4) {
+      order(2, 3);
+      order(0, 2);
+      order(1, 3);
+      order(1, 2);
+    }
+    int next = 0;
+    for (int j = 0; j < top; ++j) {
+      uint64_t offer = 0ull;
+#pragma unroll
+      for (int it = kIter - 1; it >= 0; --it) offer = next == it ? key[it] : offer;
+      uint64_t best = offer;
+      max_key_step<16>(best);
+      max_key_step<8>(best);
+      max_key_step<4>(best);
+      max_key_step<2>(best);
+      max_key_step<1>(best);
+      if (best != 0ull && offer == best) ++next;
+      if (lane == j) {
+        picked = best != 0ull ? __uint_as_float(static_cast<uint32_t>(best >> 32)) : -1.0f;
+        picked_expert = best != 0ull ? static_cast<int>(~static_cast<uint32_t>(best)) : INT_MAX;
+      }
+    }
+  } else {
   uint32_t taken = 0u;
   const uint64_t half_lanes = (lane_id() & kHalf) ? 0xffffffff00000000ull : 0x00000000ffffffffull;
   for (int j = 0; j < top; ++j) {
@@ -196,6 +249,7 @@ __device__ __forceinline__ int32_t route(const void *scores, int score_kind, int
       picked_expert = best_expert;
     }
     if (best_expert != INT_MAX && (best_expert & (kHalf - 1)) == lane) taken |= 1u << (best_expert / kHalf);
+  }
   }
 
   float weight = picked;
