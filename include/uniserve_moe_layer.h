@@ -131,7 +131,8 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_
 ///   layer does not skip it, plus the hidden rows' e4m3 / MXFP8 quantisation for those weights -
 ///   and TOPK, SORT and QUANTIZE_HIDDEN launch nothing;
 /// - prefill sizes (at most 128 experts, hidden a multiple of 128): ROUTER launches router scores,
-///   topk and the hidden rows' quantisation in one kernel, TOPK launches nothing, SORT the sort,
+///   topk and the hidden rows' quantisation in one kernel (in a call that also runs SORT, the sort's
+///   per-chunk counts too, so that SORT launches only its placement), TOPK launches nothing, SORT the sort,
 ///   and QUANTIZE_HIDDEN only the copy of each token's scales to its routes' rows where the
 ///   products take them route-major (views.route_scales);
 /// - otherwise each step launches its own operator.

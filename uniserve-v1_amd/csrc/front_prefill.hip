@@ -31,6 +31,7 @@ namespace {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kTokens = 32;             // tokens per workgroup: one per 32-lane half
+static_assert(kTokens == kFrontChunkTokens, "the sort's chunks are the workgroups' tokens");
 constexpr int kExperts = 128;           // router rows the LDS holds
 constexpr int kRowBytes = 256;          // 128 bf16 channels per row and stage
 constexpr int kSlots = 4;               // stages in flight: three ahead of the one being read
@@ -180,7 +181,9 @@ __global__ void __launch_bounds__(kThreads) prefill_front_kernel(PrefillFrontPar
     quantize_stage(k);
   }
   prefill::wait_all_loads();
-  __syncthreads();  // the ring is free: the scores tile goes over it
+  __syncthreads();  // the ring is free: the scores tile goes over it, the chunk's counts after it
+  int32_t *held = reinterpret_cast<int32_t *>(lds + kTokens * kExperts * 2);
+  if (p.chunk_counts != nullptr && static_cast<int>(threadIdx.x) < p.local_experts) held[threadIdx.x] = 0;
 
   // Lane (r16, g) holds token 16 tb + r16 and experts 16 eb + 4 g .. + 3.
   uint16_t *scores = reinterpret_cast<uint16_t *>(lds);
@@ -206,9 +209,22 @@ __global__ void __launch_bounds__(kThreads) prefill_front_kernel(PrefillFrontPar
   const bool active = token < p.tokens;
   // Four slots per lane whatever the expert count (at most 128): the slots past it hold -inf and
   // add exact zeros, so the picks and weights are those of the smallest slot count.
-  topk::route<kExperts / topk::kHalf, false>(scores, 1, experts, static_cast<int>(active ? token : 0), experts, p.top,
-                                            p.renormalize, nullptr, -1, p.ids, p.weights, p.map, p.live, p.load,
-                                            active, local);
+  const int32_t id = topk::route<kExperts / topk::kHalf, false>(
+      scores, 1, experts, static_cast<int>(active ? token : 0), experts, p.top, p.renormalize, nullptr, -1, p.ids,
+      p.weights, p.map, p.live, p.load, active, local);
+
+  // The sort's count of this chunk of tokens: lane k < top of an active token holds route
+  // token * top + k's id (the one stored).
+  if (p.chunk_counts != nullptr) {
+    const int k = static_cast<int>(threadIdx.x) & (topk::kHalf - 1);
+    const int64_t live = (p.live != nullptr ? static_cast<int64_t>(p.live[0]) : p.tokens) * p.top;
+    const int64_t slot = static_cast<int64_t>(id) - p.local_offset;
+    if (active && k < p.top && token * p.top + k < live && slot >= 0 && slot < p.local_experts)
+      atomicAdd(held + slot, 1);
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < p.local_experts)
+      p.chunk_counts[static_cast<int64_t>(blockIdx.x) * p.local_experts + threadIdx.x] = held[threadIdx.x];
+  }
 }
 
 /// One thread per (permuted row, word), rows fastest: the stores of a word run along the rows.

@@ -83,6 +83,11 @@ struct PrefillFrontParams {
   uint8_t *codes;
   float *scales;
   uint8_t *mx_scales;
+  /// Or null: each workgroup's held routes per local expert ([workgroups, local_experts]; a route
+  /// is held when it is live and its id lies in [local_offset, local_offset + local_experts)) -
+  /// the sort's count of the workgroup's 32 tokens (kFrontChunkTokens).
+  int32_t *chunk_counts;
+  int32_t local_offset, local_experts;
 };
 
 /// Whether one launch serves these extents: at most 128 experts picking at most 32, whole

@@ -116,9 +116,11 @@ extern "C" int64_t uniserve_moe_layer_workspace(int64_t tokens, int64_t hidden_s
 namespace {
 
 /// moe_sort over the window's experts, as the layer calls it.
+/// `counted`: the prefill front end wrote its chunks' counts to `scratch` (only with the two-launch
+/// sort: prefill_counts_sort).
 int32_t run_sort(const uniserve_moe_layer_call *call, int32_t *ids, float *weights, int32_t *t2e, int32_t *t2l,
                  int32_t *e2p, int32_t *p2e, int32_t *p2t, int32_t *padded, int32_t *tiles, int64_t local_experts,
-                 int32_t *scratch, void *stream) {
+                 int32_t *scratch, void *stream, bool counted = false) {
   const int64_t routes = call->tokens * call->top;
   if (scratch != nullptr && uniserve::layer_sort_two_launches(routes, local_experts)) {
     // Above one workgroup's routes: the count, then the scan folded into the placement, with the
@@ -141,7 +143,7 @@ int32_t run_sort(const uniserve_moe_layer_call *call, int32_t *ids, float *weigh
     int bits = 0;
     while ((1ll << bits) <= local_experts) ++bits;
     p.key_bits = bits;
-    uniserve::launch_layer_sort(p, scratch, static_cast<hipStream_t>(stream));
+    uniserve::launch_layer_sort(p, scratch, static_cast<hipStream_t>(stream), counted);
     return uniserve::launched(call, "moe_sort");
   }
   uniserve_moe_sort_call sort{};
@@ -366,7 +368,7 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     // The sort's per-chunk counts: the last bytes of the products' rows, which only FC2 writes,
     // later (the MXFP4 prefill front end parks its token-major scales at their start).
     const int64_t products_bytes = v.permuted_rows * call->hidden_size * 2;
-    const int64_t sort_bytes = (layer_sort_scratch_bytes(call->tokens * call->top, local_experts) + 255) / 256 * 256;
+    const int64_t sort_bytes = (layer_sort_scratch_bytes(call->tokens, call->top, local_experts) + 255) / 256 * 256;
     int32_t *sort_scratch =
         sort_bytes + call->tokens * (call->hidden_size / 32) <= products_bytes
             ? reinterpret_cast<int32_t *>(static_cast<char *>(at(v.products)) + products_bytes - sort_bytes)
@@ -425,8 +427,17 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         if (int32_t status = launched(call, "router, topk and sort")) return status;
       }
     } else if (prefill_front) {
+      // A call that runs both steps lets the front end count the sort's chunks (SORT then launches
+      // the placement alone); a SORT step on its own counts again from the ids.
+      const bool front_counts = want(UNISERVE_MOE_LAYER_ROUTER) && want(UNISERVE_MOE_LAYER_SORT) &&
+                                sort_scratch != nullptr && layer_sort_two_launches(routes, local_experts);
       if (want(UNISERVE_MOE_LAYER_ROUTER)) {
         PrefillFrontParams pp{};
+        if (front_counts) {
+          pp.chunk_counts = sort_scratch;
+          pp.local_offset = static_cast<int32_t>(call->local_offset);
+          pp.local_experts = static_cast<int32_t>(local_experts);
+        }
         pp.x = static_cast<const uint16_t *>(call->hidden);
         pp.w = static_cast<const uint16_t *>(call->router);
         pp.bias = call->router_bias;
@@ -454,7 +465,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         if (int32_t status = launched(call, "router and topk")) return status;
       }
       if (want(UNISERVE_MOE_LAYER_SORT)) {
-        if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, sort_scratch, stream))
+        if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, sort_scratch,
+                                      stream, front_counts))
           return status;
       }
     } else {

@@ -383,8 +383,9 @@ inline size_t scan_place_lds_bytes(int64_t local_experts) {
   return static_cast<size_t>((kSplitWaves + 3 + 2 * scan_place_parts(local_experts)) * local_experts) * sizeof(int32_t);
 }
 
-template <int64_t kChunkRoutes>
-__global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortParams p, const int32_t *counts) {
+/// Chunk b is routes [b chunk_routes, (b + 1) chunk_routes), the last one up to the last route.
+__global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortParams p, const int32_t *counts,
+                                                                        int64_t chunk_routes, int64_t chunks) {
   extern __shared__ int32_t lds[];
   const int E = p.local_experts;
   const int parts = scan_place_parts(E);
@@ -398,7 +399,6 @@ __global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortPara
   const int lane = lane_id();
   const uint64_t below = (1ull << lane) - 1ull;
   const int64_t live = p.live_tokens == nullptr ? p.routes : static_cast<int64_t>(p.live_tokens[0]) * p.top;
-  const int64_t chunks = p.routes / kChunkRoutes;
   const int64_t own = blockIdx.x;
   constexpr int kBatchChunks = 16;
 
@@ -480,7 +480,8 @@ __global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortPara
   }
 
   int64_t first, past, slice_first, slice_past;
-  split_chunk<kChunkRoutes>(p, &first, &past);
+  first = own * chunk_routes;
+  past = own + 1 == chunks ? p.routes : first + chunk_routes;
   split_count(p, first, past, live, wave_rows, &slice_first, &slice_past);
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += kSplitThreads) {
@@ -518,16 +519,24 @@ bool layer_sort_two_launches(int64_t routes, int64_t local_experts) {
   return routes > sort::kChunk && 2 * local_experts <= kSplitChunk;
 }
 
-int64_t layer_sort_scratch_bytes(int64_t routes, int64_t local_experts) {
-  return routes / kLayerChunk * local_experts * static_cast<int64_t>(sizeof(int32_t));
+int64_t layer_sort_scratch_bytes(int64_t tokens, int64_t top, int64_t local_experts) {
+  const int64_t counted = tokens * top / kLayerChunk;                 // the count launch's chunks
+  const int64_t front = ceil_div<int64_t>(tokens, kFrontChunkTokens);  // the prefill front end's
+  return (counted > front ? counted : front) * local_experts * static_cast<int64_t>(sizeof(int32_t));
 }
 
-void launch_layer_sort(const sort::SortParams &p, int32_t *counts, hipStream_t stream) {
-  const uint32_t chunks = static_cast<uint32_t>(p.routes / kLayerChunk);
+void launch_layer_sort(const sort::SortParams &p, int32_t *counts, hipStream_t stream, bool counted) {
+  // The prefill front end counts its own chunks (kFrontChunkTokens tokens each); otherwise the
+  // count launch does, over kLayerChunk routes.
+  const int64_t chunk_routes = counted ? kFrontChunkTokens * p.top : kLayerChunk;
+  const int64_t chunks = counted ? ceil_div<int64_t>(p.routes, chunk_routes) : p.routes / kLayerChunk;
   const size_t count_bytes = kSplitWaves * p.local_experts * sizeof(int32_t);
-  hipLaunchKernelGGL((sort_count_kernel<kLayerChunk>), dim3(chunks), dim3(kSplitThreads), count_bytes, stream, p, counts);
-  hipLaunchKernelGGL((sort_scan_place_kernel<kLayerChunk>), dim3(chunks), dim3(kSplitThreads),
-                     scan_place_lds_bytes(p.local_experts), stream, p, static_cast<const int32_t *>(counts));
+  if (!counted)
+    hipLaunchKernelGGL((sort_count_kernel<kLayerChunk>), dim3(static_cast<uint32_t>(chunks)), dim3(kSplitThreads),
+                       count_bytes, stream, p, counts);
+  hipLaunchKernelGGL(sort_scan_place_kernel, dim3(static_cast<uint32_t>(chunks)), dim3(kSplitThreads),
+                     scan_place_lds_bytes(p.local_experts), stream, p, static_cast<const int32_t *>(counts), chunk_routes,
+                     chunks);
 }
 
 }  // namespace uniserve

@@ -180,8 +180,12 @@ __device__ __forceinline__ void small_sort(const SortParams &p, int32_t *lds) {
 /// The layer's sort above one workgroup's routes, in two launches (count, then the scan folded
 /// into the placement) with the per-chunk counts in a scratch table of layer_sort_scratch_bytes
 /// that nothing else reads or writes meanwhile; the maps are the moe_sort entry's bit for bit.
+/// `counted`: the prefill front end has already written the counts of its chunks of
+/// kFrontChunkTokens tokens ([chunks, local experts], the held routes per local expert), and only
+/// the placement launches.
+constexpr int64_t kFrontChunkTokens = 32;
 bool layer_sort_two_launches(int64_t routes, int64_t local_experts);
-int64_t layer_sort_scratch_bytes(int64_t routes, int64_t local_experts);
-void launch_layer_sort(const sort::SortParams &p, int32_t *counts, hipStream_t stream);
+int64_t layer_sort_scratch_bytes(int64_t tokens, int64_t top, int64_t local_experts);
+void launch_layer_sort(const sort::SortParams &p, int32_t *counts, hipStream_t stream, bool counted);
 
 }  // namespace uniserve
