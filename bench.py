@@ -281,7 +281,7 @@ def traffic_summary(directory):
     import re
 
     products = {"gather_gemm": "true", "route_gemm": "false"}
-    pattern = re.compile(r"((?:stream|prefill|tiled|pair)\w*)<([^<>]*)>\(")
+    pattern = re.compile(r"((?:stream|prefill|tiled|pair|quarter)\w*)(?:<([^<>]*)>)?\(")
     configs = {}
     for name in CONFIGS:
         if not (root / name).exists():
@@ -291,6 +291,8 @@ def traffic_summary(directory):
         entry = {}
         for product, gated in products.items():
             def gated_flag(match):  # prefill_kernel / pair_kernel<format, gated>; the others <gated, ...>
+                if match.group(2) is None:  # quarter_kernel: FC1 only
+                    return "true"
                 args = [a.strip() for a in match.group(2).split(",")]
                 return args[-1] if match.group(1).startswith(("prefill", "pair")) else args[0]
 
@@ -299,7 +301,8 @@ def traffic_summary(directory):
                 continue
             kernel, match = found[0]
             f, wr = fetch[kernel], write.get(kernel, 0.0)
-            entry[product] = {"kernel": f"{match.group(1)}<{match.group(2).replace('uniserve::', '')}>",
+            args = "" if match.group(2) is None else f"<{match.group(2).replace('uniserve::', '')}>"
+            entry[product] = {"kernel": f"{match.group(1)}{args}",
                               "fetch_KiB": round(f, 1),
                               "write_KiB": round(wr, 1),
                               "hbm_bytes": int(f * 1024 * fetch_scale + wr * 1024 * write_scale)}

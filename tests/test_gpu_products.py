@@ -42,6 +42,7 @@ CASES = {
     "tiny": (16, 256, 8, 2, 128, "uniform"),
     "235b decode one token": (1, 4096, 128, 8, 1536, "uniform"),
     "odd widths (tiled, 64-column slices)": (300, 320, 16, 4, 192, "uniform"),
+    "stream, hidden not a multiple of 256 (row-sliced FC1)": (16, 320, 16, 4, 192, "uniform"),
 }
 
 

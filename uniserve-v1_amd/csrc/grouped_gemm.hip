@@ -279,6 +279,143 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   }
 }
 
+// ---- quarter kernel (decode, expert-major) ----------------------------------------------------------------
+//
+// FC1's gated product with the workgroup's 128 weight rows (64 up + the matching 64 gate rows)
+// streamed by every wavefront over its own quarter of K: wavefront q walks K
+// lines q K / 256 .. (q + 1) K / 256 - 1 (64 bf16 each) of all 128 rows, one step = one line of 64
+// rows (8 instructions of 8 rows x 128 bytes), the two halves of the rows in turn. At any moment
+// the workgroup's four wavefronts read four neighbouring stretches of the same rows, which DRAM
+// serves from fewer row openings than the row-sliced walk, where each wavefront reads 256 bytes of
+// its own rows per stage (a bare kernel reading FC1's weights: 7.2 against 6.3 TB/s). Each
+// wavefront holds partial sums of all 128 rows; at the end they meet in LDS and wavefront w adds
+// the four in wave order for its output rows (up set w and gate set w + 4: 16 gated columns).
+// FC1 from 124 to 120 us at 30B T=64; FC2 (128 rows of one kind) measured 1 us slower, so it keeps
+// the row-sliced kernel. Needs K % 256 == 0 and byte offsets of an expert's weights and of the
+// activations below 2^32.
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) quarter_kernel(GroupedParams p) {
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  int64_t expert = blockIdx.x;
+  if (p.compact) {
+    __shared__ uint32_t named[kPresentExperts / 32];
+    const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+    expert = nth_named_expert<kThreads>(p.ids, p.routes, live, static_cast<int32_t>(p.local_offset),
+                                        static_cast<int32_t>(p.local_experts), static_cast<int>(blockIdx.x), named);
+    if (expert < 0) return;
+  }
+  // Row r (0..127) of the workgroup: up row slice * 64 + r, or gate row I + slice * 64 + r - 64.
+  const int64_t slice = blockIdx.y;
+  auto weight_row = [&](int r) -> int64_t { return r < 64 ? slice * 64 + r : p.out_width + slice * 64 + (r - 64); };
+  const int lines = static_cast<int>(p.K / 64);       // 128-byte lines per row
+  const int per_wave = lines / kWaves;                // this wavefront's lines: [wave * per_wave, ..)
+  const int steps = 2 * per_wave;                     // (line, half of the rows)
+  // Step t: line wave * per_wave + t / 2 of rows 64 (t % 2) + 8 i + l / 8, chunk l % 8. The rows of
+  // a half are consecutive, so load i's address is a uniform base (the expert's stack, 8 i rows on,
+  // the step's line) plus one 32-bit lane offset per half: few registers per address.
+  expert = __builtin_amdgcn_readfirstlane(static_cast<int>(expert));
+  const uint8_t *wbase = reinterpret_cast<const uint8_t *>(p.weights + expert * p.n_total * p.K);
+  const int64_t row_bytes = p.K * 2;
+  uint32_t half_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    half_off[h] = static_cast<uint32_t>(weight_row(64 * h + lane / 8) * row_bytes + wave * per_wave * 128 + (lane & 7) * 16);
+  struct Step {
+    u32x4 lines[8];
+  };
+  auto load_step = [&](Step &st, int t) {
+    const int h = t & 1;
+    const uint8_t *line = wbase + static_cast<int64_t>(t >> 1) * 128;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      st.lines[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(line + static_cast<int64_t>(i) * 8 * row_bytes + half_off[h]));
+  };
+  Step even, odd;
+  load_step(even, 0);  // no dependence on the routes: out before the scan
+
+  __shared__ u32x4 regroup[kWaves][8 * 64];
+  __shared__ int32_t route_list[kExpertRoutes];
+  __shared__ int32_t wave_count[kWaves + 1];
+  const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
+  const int rows = list_expert_routes<kWaves>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
+                                              route_list, wave_count);
+  if (rows == 0) return;
+  auto listed = [&](int m) -> int64_t { return listed_route<kWaves>(route_list, wave_count, p.routes, m); };
+
+  for (int pass = 0; pass < rows; pass += 16) {
+    const int m = pass + r16;
+    const bool valid = m < rows;
+    const int64_t source = valid ? listed(m) / p.top : 0;
+    // Rows past the expert's routes read row 0 (never stored).
+    const uint32_t a_off = static_cast<uint32_t>((source * p.K + static_cast<int64_t>(wave) * per_wave * 64 + g * 8) * 2);
+    const uint8_t *act = reinterpret_cast<const uint8_t *>(p.act);
+    floatx4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 x[2][2];  // [line parity][K step of 32]: this lane's 8 elements of each
+    auto load_x = [&](int line, u32x4 (&into)[2]) {
+      into[0] = *reinterpret_cast<const u32x4 *>(act + static_cast<int64_t>(line) * 128 + a_off);
+      into[1] = *reinterpret_cast<const u32x4 *>(act + static_cast<int64_t>(line) * 128 + 64 + a_off);
+    };
+    auto compute = [&](const Step &st, int t, const u32x4 (&xs)[2]) {
+      {
+        const int row = lane >> 3, piece = lane & 7;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) regroup[wave][i * 64 + row * 8 + (piece ^ row)] = st.lines[i];
+      }
+      const int h = t & 1;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 2 * j + (r16 >> 3), rr = r16 & 7, q = 4 * ks + g;
+          const u32x4 w = regroup[wave][i * 64 + rr * 8 + (q ^ rr)];
+          acc[4 * h + j] = mfma_16x16x32_bf16(w, xs[ks], acc[4 * h + j]);
+        }
+    };
+    if (pass > 0) load_step(even, 0);
+    load_x(0, x[0]);
+    // Steps in pairs (both halves of one line); the next pair's loads go out before this pair's
+    // computes wait, all unconditionally in the steady walk.
+    int t = 0;
+    for (; t + 2 < steps; t += 2) {
+      load_step(odd, t + 1);
+      load_x((t >> 1) + 1, x[1]);
+      compute(even, t, x[0]);
+      load_step(even, t + 2);
+      compute(odd, t + 1, x[0]);
+      x[0][0] = x[1][0];
+      x[0][1] = x[1][1];
+    }
+    load_step(odd, t + 1);
+    compute(even, t, x[0]);
+    compute(odd, t + 1, x[0]);
+
+    // The four quarters' partial sums, added in wave order; each wavefront's go through its own
+    // regroup buffer (8 x 64 floatx4, the buffer's size), which it no longer reads.
+    auto partial = [&](int w, int j) -> floatx4 & { return reinterpret_cast<floatx4 *>(regroup[w])[j * kWave + lane]; };
+#pragma unroll
+    for (int j = 0; j < 8; ++j) partial(wave, j) = acc[j];
+    __syncthreads();
+    floatx4 up = partial(0, wave), gated = partial(0, wave + 4);
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      up += partial(w, wave);
+      gated += partial(w, wave + 4);
+    }
+    __syncthreads();  // the next pass regroups over the partial sums
+    if (valid) {
+      floatx4 hv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hv[i] = gate(gated[i], p.activation) * up[i];
+      store_bf16x4(p.out + listed(m) * p.out_width + slice * 64 + wave * 16 + 4 * g, hv);
+    }
+  }
+}
+
 // ---- tiled kernel -----------------------------------------------------------------------------------------
 
 constexpr int kBK = 64;               // K elements per stage: 8 chunks of 16 bytes per row
@@ -465,6 +602,11 @@ void launch_expert_stream(const ExpertStream &e, bool gated, hipStream_t stream)
   const bool one_pass = e.routes <= kOnePassRowsPerExpert * e.local_experts;
   const int64_t slices = gated ? e.out_width / 64 : e.out_width / 128;
   const dim3 grid(static_cast<uint32_t>(p.compact ? e.routes : e.local_experts), static_cast<uint32_t>(slices));
+  constexpr int64_t kOffsetRange = int64_t{1} << 32;  // the quarter kernel's 32-bit byte offsets
+  if (gated && e.K % 256 == 0 && e.n_total * e.K * 2 < kOffsetRange && e.routes * e.K * 2 < kOffsetRange) {
+    hipLaunchKernelGGL(quarter_kernel, grid, dim3(kThreads), 0, stream, p);
+    return;
+  }
   if (gated && one_pass) hipLaunchKernelGGL((stream_kernel<true, 1, true>), grid, dim3(kThreads), 0, stream, p);
   else if (gated) hipLaunchKernelGGL((stream_kernel<true, 2, true>), grid, dim3(kThreads), 0, stream, p);
   else if (one_pass) hipLaunchKernelGGL((stream_kernel<false, 1, true>), grid, dim3(kThreads), 0, stream, p);
