@@ -160,6 +160,16 @@ def test_product_refusals():
         c.tokens += 1
         assert entry(ctypes.byref(c), None) != 0 and "below 4 GiB" in message(c)
 
+    # The MXFP4 FC2's stream kernel (few routes per expert) addresses every permuted row from the
+    # array's base with 32-bit offsets: rows past 4 GiB are refused before any launch.
+    m = abi.RouteMxCall()
+    for name in ("rows", "row_scales", "weights", "weight_scales", "out", "tile_to_expert", "tile_to_limit",
+                 "permuted_to_expanded", "num_non_exiting_tiles"):
+        setattr(m, name, ctypes.addressof(buf))
+    m.out_dtype, m.multiprocessors, m.intermediate, m.width, m.experts = abi.DTYPE["bf16"], 256, 1536, 2048, 1 << 16
+    m.permuted_rows = 128 * ((1 << 32) // (1536 * 128) + 1)  # just past 4 GiB, far under 24 routes per expert
+    assert lib.uniserve_route_gemm_mx(ctypes.byref(m), None) != 0 and "below 4 GiB" in message(m)
+
     r = abi.RouteCall()
     r.dtype = abi.DTYPE["f32"]
     assert lib.uniserve_route_gemm(ctypes.byref(r), None) != 0 and "bf16 only" in message(r)

@@ -920,10 +920,16 @@ int32_t route_gemm_mx(const uniserve_route_mx_call *call, int64_t scale_rows, vo
     p.as_by_route = scale_rows != 0 ? 1 : 0;
     // No token count in the call: the permuted rows less one partial tile per expert bound the routes.
     const int64_t routes_bound = call->permuted_rows - (kTileRows - 1) * call->experts;
-    if (!fp8_stream_path(routes_bound, call->experts) && tiled_fits(false, p.K, p.out_width))
+    if (!fp8_stream_path(routes_bound, call->experts) && tiled_fits(false, p.K, p.out_width)) {
       launch_tiled_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
-    else
+    } else {
+      // The stream kernel addresses every permuted row from the arrays' bases (32-bit offsets; the
+      // scales, K / 32 bytes a row, take fewer bytes than the codes).
+      if (!dma_rows_fit(call->permuted_rows, p.K))
+        return UNISERVE_REFUSE(call, "route_gemm_mx serves rows below 4 GiB on its stream kernel (%lld rows of %lld bytes)",
+                               static_cast<long long>(call->permuted_rows), static_cast<long long>(p.K));
       launch_mx(p, false, max_tiles, static_cast<hipStream_t>(stream));
+    }
     return launched(call, "route_gemm_mx");
   });
 }
