@@ -106,7 +106,9 @@ constexpr int64_t kSplitBelow = 512;  // stream workgroups under which K is spli
 /// Decode-shaped: as the bf16 stream kernel, one 128-deep scale block per chunk. kSplit: the four
 /// wavefronts share one row set and split K (scale block kb goes to wave kb % 4), their partial sums
 /// meeting in LDS in wave order - four times the workgroups, for batches whose tiles x slices would
-/// leave most of the chip idle (a single token: 8 tiles).
+/// leave most of the chip idle (a single token: 8 tiles). Both sets' lines of a block go out
+/// together, as in the unsplit form (walking the two sets in turn, half the lines in flight: 235B
+/// T=1 FC1 18.5 against 18.3 us, FC2 12.7 against 12.2, the same sums).
 /// kPassTiles: rows of a tile one pass covers, in MFMA blocks of 16.
 /// kByExpert: workgroup x serves local expert x and lists its rows itself (the routes naming it in
 /// `ids`, route order), reading act row route / top (FC1) or route (FC2) and writing row `route`.
@@ -194,8 +196,8 @@ __global__ void __launch_bounds__(kWaves * kWave) stream_fp8_kernel(GroupedFp8Pa
 
   // Expert-major: the first weight block goes out before the route scan (it depends on nothing the
   // routes decide), then the scan lists the expert's rows.
-  u32x4 wcur[4], wnext[4];  // the unsplit form's weight lines of alternate blocks
-  if constexpr (kByExpert && !kSplit) {
+  u32x4 wcur[4], wnext[4];  // the weight lines of alternate blocks
+  if (kByExpert && kb_first < kb_count) {  // (a split wave may own no block)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       wcur[i] = __builtin_nontemporal_load(
@@ -282,80 +284,11 @@ __global__ void __launch_bounds__(kWaves * kWave) stream_fp8_kernel(GroupedFp8Pa
           for (int i = 0; i < 4; ++i) acc[set][ms][i] = __builtin_fmaf(block[i], scale, acc[set][ms][i]);
         }
     };
-    if constexpr (kSplit) {
-      // The split form walks its two 16-row sets one after the other: two weight lines per scale
-      // block in flight instead of four, so the kernel holds fewer registers and more waves per
-      // SIMD (measured when it was three against two) - a single token's 768 workgroups (235B FC1) then run
-      // in one round (FC1 26 -> 22 us). At 64 tokens the unsplit kernel keeps both sets in flight
-      // (walking them in turn there re-reads the activations: FC1 65 -> 77 us).
-      struct Block {
-        u32x4 w[2];
-        intx8 x[kPassTiles];
-        float s[1 + kPassTiles];
-      };
-      for (int set = 0; set < 2; ++set) {
-        const float *ws = set == 0 ? ws0 : ws1;
-        auto fetch1 = [&](int64_t kb, Block &d) {
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            d.w[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(line_row[set] + static_cast<int64_t>(i) * 8 * p.K + kb * 128));
-          d.s[0] = ws[kb];
-#pragma unroll
-          for (int ms = 0; ms < kPassTiles; ++ms) {
-            const u32x4 lo = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128);
-            const u32x4 hi = *reinterpret_cast<const u32x4 *>(a[ms] + kb * 128 + 64);
-            d.x[ms] = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
-                            static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-            d.s[1 + ms] = as[ms][kb];
-          }
-        };
-        auto compute1 = [&](const Block &d) {
-          {
-            const int row = lane >> 3, piece = lane & 7;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) regroup[wave][i * 64 + row * 8 + (piece ^ row)] = d.w[i];
-          }
-          const int rr = r16 & 7, li = r16 >> 3;
-          const u32x4 lo = regroup[wave][li * 64 + rr * 8 + (g ^ rr)];
-          const u32x4 hi = regroup[wave][li * 64 + rr * 8 + ((g + 4) ^ rr)];
-          const intx8 w = intx8{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3]),
-                                static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
-#pragma unroll
-          for (int ms = 0; ms < kPassTiles; ++ms) {
-            const floatx4 block = mfma_16x16x128_fp8(w, d.x[ms], floatx4{0.0f, 0.0f, 0.0f, 0.0f});
-            const float scale = d.s[0] * d.s[1 + ms];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[set][ms][i] = __builtin_fmaf(block[i], scale, acc[set][ms][i]);
-          }
-        };
-        Block cur, next;
-        // (Unconditional loads in the steady walk, the last blocks peeled: see the unsplit walk.)
-        int64_t kb = kb_first;
-        if (kb < kb_count) {
-          fetch1(kb, cur);
-          for (; kb + 2 * kb_step < kb_count; kb += 2 * kb_step) {
-            fetch1(kb + kb_step, next);
-            compute1(cur);
-            fetch1(kb + 2 * kb_step, cur);
-            compute1(next);
-          }
-          if (kb + kb_step < kb_count) {
-            fetch1(kb + kb_step, next);
-            compute1(cur);
-            compute1(next);
-          } else {
-            compute1(cur);
-          }
-        }
-      }
-    } else {
     intx8 acur[kPassTiles], anext[kPassTiles];
     float scur[2 + kPassTiles], snext[2 + kPassTiles];
-    if (kByExpert && pass == 0 && run == 0) {
-      fetch_rest(kb_first, acur, scur);  // its weight lines went out before the route scan
-    } else if (kb_first < kb_count) {
-      fetch(kb_first, wcur, acur, scur);
+    if (kb_first < kb_count) {
+      if (kByExpert && pass == 0 && run == 0) fetch_rest(kb_first, acur, scur);  // lines out before the scan
+      else fetch(kb_first, wcur, acur, scur);
     }
     // The steady walk issues both blocks' loads unconditionally, so the compiler's wait before
     // each compute counts exactly the other block's loads still in flight (with the loads under
@@ -376,7 +309,6 @@ __global__ void __launch_bounds__(kWaves * kWave) stream_fp8_kernel(GroupedFp8Pa
       } else {
         compute(wcur, acur, scur);
       }
-    }
     }
     if constexpr (kSplit) {
       // Waves 1..3 hand their partial sums to wave 0, which adds them in wave order.
