@@ -134,7 +134,8 @@ UNISERVE_EXTERN_C int32_t uniserve_moe_layer_no_alloc(const struct uniserve_moe_
 ///   topk and the hidden rows' quantisation in one kernel (in a call that also runs SORT, the sort's
 ///   per-chunk counts too, so that SORT launches only its placement), TOPK launches nothing, SORT the sort,
 ///   and QUANTIZE_HIDDEN only the copy of each token's scales to its routes' rows where the
-///   products take them route-major (views.route_scales);
+///   products take them route-major (views.route_scales) and the sort's placement has not made
+///   it (the placement makes it for more than 4096 routes, hidden a multiple of 512 up to 4096);
 /// - otherwise each step launches its own operator.
 /// The quantiser steps launch nothing for bf16 weights, and QUANTIZE_GATED nothing where FC1
 /// writes its rows already quantised (e4m3 at prefill sizes; MXFP4 with route-major scales; and, for

@@ -117,10 +117,12 @@ namespace {
 
 /// moe_sort over the window's experts, as the layer calls it.
 /// `counted`: the prefill front end wrote its chunks' counts to `scratch` (only with the two-launch
-/// sort: prefill_counts_sort).
+/// sort: prefill_counts_sort). `words` (two-launch sort only): token_words' `words` 32-bit words per
+/// token go to each route's row of route_words ([words, word_rows]) as the placement places it.
 int32_t run_sort(const uniserve_moe_layer_call *call, int32_t *ids, float *weights, int32_t *t2e, int32_t *t2l,
                  int32_t *e2p, int32_t *p2e, int32_t *p2t, int32_t *padded, int32_t *tiles, int64_t local_experts,
-                 int32_t *scratch, void *stream, bool counted = false) {
+                 int32_t *scratch, void *stream, bool counted = false, const uint32_t *token_words = nullptr,
+                 uint32_t *route_words = nullptr, int64_t words = 0, int64_t word_rows = 0) {
   const int64_t routes = call->tokens * call->top;
   if (scratch != nullptr && uniserve::layer_sort_two_launches(routes, local_experts)) {
     // Above one workgroup's routes: the count, then the scan folded into the placement, with the
@@ -143,6 +145,10 @@ int32_t run_sort(const uniserve_moe_layer_call *call, int32_t *ids, float *weigh
     int bits = 0;
     while ((1ll << bits) <= local_experts) ++bits;
     p.key_bits = bits;
+    p.token_words = token_words;
+    p.route_words = route_words;
+    p.words = words;
+    p.word_rows = word_rows;
     uniserve::launch_layer_sort(p, scratch, static_cast<hipStream_t>(stream), counted);
     return uniserve::launched(call, "moe_sort");
   }
@@ -373,6 +379,12 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         sort_bytes + call->tokens * (call->hidden_size / 32) <= products_bytes
             ? reinterpret_cast<int32_t *>(static_cast<char *>(at(v.products)) + products_bytes - sort_bytes)
             : nullptr;
+    // Prefill e4m3 / MXFP4 with route-major scales: the two-launch sort's placement copies each
+    // token's scales (token-major, from the front end) to its routes' rows (QUANTIZE_HIDDEN then
+    // launches nothing); the one-workgroup sort leaves the copy to QUANTIZE_HIDDEN.
+    const bool sort_scatters = prefill_quantizes && v.route_scales && sort_scratch != nullptr &&
+                               layer_sort_two_launches(routes, local_experts) && call->hidden_size % 512 == 0 &&
+                               call->hidden_size / 128 <= sort::kMaxRouteWords;
 
     // Decode sizes: router, topk and sort in one launch (at the ROUTER step; TOPK and SORT launch
     // nothing).
@@ -465,8 +477,16 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
         if (int32_t status = launched(call, "router and topk")) return status;
       }
       if (want(UNISERVE_MOE_LAYER_SORT)) {
+        // The front end's token-major scale words go route-major as the placement places each route.
+        const uint32_t *token_words = nullptr;
+        uint32_t *route_words = nullptr;
+        if (sort_scatters) {
+          token_words = static_cast<const uint32_t *>(at(fp8 ? v.hidden_s : v.products));
+          route_words = static_cast<uint32_t *>(at(fp8 ? v.hidden_route_s : v.hidden_s));
+        }
         if (int32_t status = run_sort(call, ids, weights, t2e, t2l, e2p, p2e, p2t, padded, tiles, local_experts, sort_scratch,
-                                      stream, front_counts))
+                                      stream, front_counts, token_words, route_words, call->hidden_size / 128,
+                                      v.permuted_rows))
           return status;
       }
     } else {
@@ -500,7 +520,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
     if (mx) {
       const ExpertRouting routing{ids, call->live_tokens, routes, call->top, call->local_offset, local_experts};
       if (int32_t status = run_mx_products(call, v, ws, want, stream, by_expert ? &routing : nullptr,
-                                                 front_quantizes || prefill_quantizes, prefill_quantizes && v.route_scales))
+                                                 front_quantizes || prefill_quantizes,
+                                                 prefill_quantizes && v.route_scales && !sort_scatters))
         return status;
     } else if (by_expert && !fp8) {
       ExpertStream e{};
@@ -579,7 +600,8 @@ int32_t run_layer(const uniserve_moe_layer_call *call, int32_t only, void *strea
       qx.width = call->hidden_size;
       qx.input_dtype = UNISERVE_DTYPE_BF16;
       qx.group = 128;
-      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || front_quantizes || (prefill_quantizes && scale_rows == 0)) {
+      if (!want(UNISERVE_MOE_LAYER_QUANTIZE_HIDDEN) || front_quantizes || (prefill_quantizes && scale_rows == 0) ||
+          sort_scatters) {
       } else if (prefill_quantizes) {
         // The prefill front end quantised the rows; each token's scales go to its routes' rows.
         launch_scatter_route_words(static_cast<const uint32_t *>(at(v.hidden_s)), p2e, padded,

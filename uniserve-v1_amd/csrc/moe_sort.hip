@@ -494,9 +494,18 @@ __global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortPara
   }
   __syncthreads();
   int32_t *mine = wave_rows + wave * E;
+  const int quads = static_cast<int>(p.words / 4);
   for (int64_t base = slice_first; base < slice_past; base += kWave) {
     const int64_t route = base + lane;
     const bool inside = route < slice_past;
+    // The route's token words, issued before its id is read (a clamped token past the slice).
+    u32x4 token_words[kMaxRouteWords / 4];
+    if (p.route_words != nullptr) {
+      const u32x4 *from = reinterpret_cast<const u32x4 *>(p.token_words + ((inside ? route : slice_first) / p.top) * p.words);
+#pragma unroll
+      for (int q = 0; q < kMaxRouteWords / 4; ++q)
+        if (q < quads) token_words[q] = from[q];
+    }
     const int32_t e = inside ? local_expert(p, route, live) : -1;
     const uint64_t peers = match_any(static_cast<uint32_t>(e + 1), p.key_bits);
     if (e >= 0) {
@@ -504,6 +513,13 @@ __global__ void __launch_bounds__(kSplitThreads) sort_scan_place_kernel(SortPara
       p.expanded_to_permuted[route] = row;
       p.permuted_to_expanded[row] = static_cast<int32_t>(route);
       p.permuted_to_token[row] = static_cast<int32_t>(route / p.top);
+      if (p.route_words != nullptr) {
+#pragma unroll
+        for (int q = 0; q < kMaxRouteWords / 4; ++q)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (q < quads) p.route_words[(4 * q + j) * p.word_rows + row] = token_words[q][j];
+      }
     } else if (inside) {
       p.expanded_to_permuted[route] = route < live ? -1 : -2;
     }

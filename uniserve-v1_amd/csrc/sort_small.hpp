@@ -14,6 +14,8 @@ constexpr int kSortWaves = kSortThreads / kWave;
 constexpr int64_t kChunk = 4096;
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
 
+constexpr int kMaxRouteWords = 32;  ///< SortParams::words: a 4096-channel row's 128-channel scales
+
 struct SortParams {
   const int32_t *ids;
   int32_t *tile_to_expert;
@@ -30,6 +32,14 @@ struct SortParams {
   int32_t local_offset;
   int32_t tile;
   int32_t key_bits;  ///< bits of (local expert + 1), the match key
+  // Optional, two-launch placement only (the layer's prefill scales): each placed route's row of
+  // route_words ([words, word_rows], rows fastest) receives its token's `words` 32-bit words from
+  // token_words ([tokens, words], 16-byte aligned rows; words a multiple of 4, at most
+  // kMaxRouteWords). Null route_words: nothing.
+  const uint32_t *token_words;
+  uint32_t *route_words;
+  int64_t words;
+  int64_t word_rows;
 };
 
 /// The local expert of route `route`, or -1 when it is not live or not in the window. kDevice: `ids`
