@@ -19,7 +19,9 @@ tensor-parallel rank ``r`` of ``n`` holds rows ``[r * I / n, (r + 1) * I / n)`` 
 projection and the same columns of each down projection (moe.rs:363-378).
 
 Everything here is host-side tensor plumbing (torch CPU or device tensors alike); nothing runs a
-kernel.
+kernel. It is a loader and test-harness helper beside the product, not part of the drop-in: the
+drop-in boundary is the C ABI (include/*.h), which takes the stacks as plain device pointers
+however they were built.
 """
 
 from dataclasses import dataclass
