@@ -18,12 +18,33 @@ __host__ __device__ constexpr int64_t routes_per_wave(int64_t routes) {
   return ((routes + kWave - 1) / kWave + kWaves - 1) / kWaves * kWave;
 }
 
+/// A wavefront's first 4 x 64 route ids of its stretch (as list_expert_routes scans it), loaded
+/// ahead: a kernel that issues its first weight loads between these loads and the scan waits for
+/// the ids alone (the wait for a load also waits for every load issued before it).
+struct FirstRouteIds {
+  int32_t id[4];
+};
+template <int kWaves>
+__device__ __forceinline__ FirstRouteIds load_first_route_ids(const int32_t *ids, int64_t routes) {
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int64_t begin = wave * routes_per_wave<kWaves>(routes);
+  FirstRouteIds first;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t route = begin + u * kWave + lane_id();
+    first.id[u] = ids[route < routes ? route : 0];  // (the scan drops routes past its stretch)
+  }
+  return first;
+}
+
 /// Lists the live routes (route < live) whose id is `want`: wavefront w ballots routes
 /// [w q, (w + 1) q), q = routes_per_wave, into list[w q ..] and counts[w]; counts[kWaves] is the
 /// total. Every thread of the workgroup calls it (two barriers); returns the total.
+/// `first`, if given: load_first_route_ids' ids, used for the stretch's first 4 x 64 routes.
 template <int kWaves>
 __device__ __forceinline__ int list_expert_routes(const int32_t *ids, int64_t routes, int64_t live, int32_t want,
-                                                  int32_t *list, int32_t *counts) {
+                                                  int32_t *list, int32_t *counts,
+                                                  const FirstRouteIds *first = nullptr) {
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int64_t per_wave = routes_per_wave<kWaves>(routes);
@@ -36,7 +57,9 @@ __device__ __forceinline__ int list_expert_routes(const int32_t *ids, int64_t ro
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t route = c + u * kWave + lane;
-      id[u] = route < end && route < live ? ids[route] : -1;
+      const bool held = route < end && route < live;
+      if (first != nullptr && c == begin) id[u] = held ? first->id[u] : -1;
+      else id[u] = held ? ids[route] : -1;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {

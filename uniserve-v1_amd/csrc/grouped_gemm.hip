@@ -174,7 +174,11 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
     }
   };
   Stage even, odd;
-  if constexpr (kByExpert) load_lines(even, 0);  // no dependence on the routes: out before the scan
+  FirstRouteIds first_ids;
+  if constexpr (kByExpert) {
+    first_ids = load_first_route_ids<kWaves>(p.ids, p.routes);
+    load_lines(even, 0);  // no dependence on the routes: out before the scan (after the ids it reads)
+  }
 
   __shared__ u32x4 regroup[kWaves][8 * 64];  // each wave's weight lines of a stage, regrouped
   // Expert-major: the route list (route order), found while the first weight stage is in flight.
@@ -183,7 +187,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(GroupedParams p) {
   if constexpr (kByExpert) {
     const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
     rows = list_expert_routes<kWaves>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
-                                      route_list, wave_count);
+                                      route_list, wave_count, &first_ids);
     if (rows == 0) return;
   }
   auto listed = [&](int m) -> int64_t { return listed_route<kWaves>(route_list, wave_count, p.routes, m); };
@@ -334,14 +338,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
           reinterpret_cast<const u32x4 *>(line + static_cast<int64_t>(i) * 8 * row_bytes + half_off[h]));
   };
   Step even, odd;
-  load_step(even, 0);  // no dependence on the routes: out before the scan
+  const FirstRouteIds first_ids = load_first_route_ids<kWaves>(p.ids, p.routes);
+  load_step(even, 0);  // no dependence on the routes: out before the scan (after the ids it reads)
 
   __shared__ u32x4 regroup[kWaves][8 * 64];
   __shared__ int32_t route_list[kExpertRoutes];
   __shared__ int32_t wave_count[kWaves + 1];
   const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
   const int rows = list_expert_routes<kWaves>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
-                                              route_list, wave_count);
+                                              route_list, wave_count, &first_ids);
   if (rows == 0) return;
   auto listed = [&](int m) -> int64_t { return listed_route<kWaves>(route_list, wave_count, p.routes, m); };
 

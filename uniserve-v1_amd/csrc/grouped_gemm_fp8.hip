@@ -197,6 +197,8 @@ __global__ void __launch_bounds__(kWaves * kWave) stream_fp8_kernel(GroupedFp8Pa
   // Expert-major: the first weight block goes out before the route scan (it depends on nothing the
   // routes decide), then the scan lists the expert's rows.
   u32x4 wcur[4], wnext[4];  // the weight lines of alternate blocks
+  FirstRouteIds first_ids;
+  if constexpr (kByExpert) first_ids = load_first_route_ids<kWaves>(p.ids, p.routes);  // (before the lines)
   if (kByExpert && kb_first < kb_count) {  // (a split wave may own no block)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -206,7 +208,7 @@ __global__ void __launch_bounds__(kWaves * kWave) stream_fp8_kernel(GroupedFp8Pa
   if constexpr (kByExpert) {
     const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
     rows = list_expert_routes<kWaves>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
-                                      route_list, route_count);
+                                      route_list, route_count, &first_ids);
     if (rows == 0) return;
   }
 

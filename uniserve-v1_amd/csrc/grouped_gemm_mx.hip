@@ -272,10 +272,11 @@ __global__ void __launch_bounds__(kThreads) stream_mx_kernel(MxParams p) {
   };
   Chunk cur, next;
   if constexpr (kByExpert) {
+    const FirstRouteIds first_ids = load_first_route_ids<kThreads / kWave>(p.ids, p.routes);  // (before the lines)
     if (!kSplit) fetch_lines(c_first, cur);  // it depends on nothing the routes decide
     const int64_t live = p.live_tokens != nullptr ? static_cast<int64_t>(p.live_tokens[0]) * p.top : p.routes;
     rows = list_expert_routes<kThreads / kWave>(p.ids, p.routes, live, static_cast<int32_t>(expert + p.local_offset),
-                                                route_list, route_count);
+                                                route_list, route_count, &first_ids);
     if (rows == 0) return;
   }
 
