@@ -940,7 +940,8 @@ namespace {
 /// FC2 (expert-major, unsplit): 128-row slices served per workgroup, one after the other. An
 /// MXFP4 FC2 slice is 48 KB of weights at 768 channels, too short a life for a workgroup: 30B
 /// T=64 FC2 31.5 us with one slice each, 30.0 with two, 28.0 with four, 36.3 with eight (FC1's
-/// 128 KB slices: 43.7 us alone, 49 in runs of two or four; the e4m3 FC2's 96 KB ones: no change).
+/// 128 KB slices: 43.7 us alone, 49 in runs of two or four; the e4m3 FC2's 96 KB ones: 34.5 us
+/// alone, 36.0 and 36.4 in runs of two and four).
 constexpr int kFc2Run = 4;
 /// The split FC2 (few routes: 32-row slices, K over the waves) likewise, two slices per workgroup:
 /// 235B T=1 FC2 14.2 -> 11.6 us by events (four: 15.9, eight: 23.2).
